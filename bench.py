@@ -1,0 +1,185 @@
+"""Benchmark of the MI355X HTDemucs backend (one JSON line on stdout).
+
+Workload ("config 3"): full htdemucs separation of a
+60 s stereo 44.1 kHz synthetic mix, fp32, random-init weights (seed 0), 7.8 s
+segments at overlap 0.25 batched 8 chunks per launch, shifts = 0. One step =
+one separation of the whole mix with the mix already resident in HBM and the
+stems written to HBM (device entry point dmx_separate_device).
+value = x-realtime = audio seconds / wall seconds over the timed steps.
+
+Also reported: the cross-attention kernel's TFLOP/s at the model's shape
+(Q 2688 vs K/V 1344, 8 heads x 64, batch 8) and its roofline fraction against
+the fp32 MFMA peak, measured with HIP events on the launch stream; and the
+restated reference CPU backend (oracle/) timed on this host on one 7.8 s
+segment.
+"""
+import argparse
+import ctypes
+import importlib.util
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+import numpy as np
+
+ROOT = Path(__file__).resolve().parent
+PACKAGE_DIR = ROOT / "demucs-wgpu_amd"
+
+FP32_MFMA_PEAK_TFLOPS = 157.3  # MI355X dense fp32 matrix peak (datasheet)
+
+
+def load_package():
+    name = "demucs_wgpu_amd"
+    if name in sys.modules:
+        return sys.modules[name]
+    spec = importlib.util.spec_from_file_location(name, PACKAGE_DIR / "__init__.py",
+                                                  submodule_search_locations=[str(PACKAGE_DIR)])
+    mod = importlib.util.module_from_spec(spec)
+    sys.modules[name] = mod
+    spec.loader.exec_module(mod)
+    return mod
+
+
+def attention_roofline(pkg, torch, batch: int, iters: int):
+    """Average duration of the fused cross-attention kernel at the model's
+    cross shape (Lq = 2688 freq tokens vs Lk = 1344 time tokens, and the
+    reverse direction), timed with events on the stream it is launched on."""
+    from demucs_wgpu_amd import _native
+    lib = _native.load()
+    heads, D = 8, 512
+    results = []
+    for lq, lk in ((2688, 1344), (1344, 2688)):
+        q = torch.randn(batch, lq, D, device="cuda")
+        k = torch.randn(batch, lk, D, device="cuda")
+        v = torch.randn(batch, lk, D, device="cuda")
+        o = torch.empty(batch, lq, D, device="cuda")
+        stream = torch.cuda.current_stream()
+        sp = ctypes.c_void_p(stream.cuda_stream)
+        args = (sp, ctypes.c_void_p(q.data_ptr()), ctypes.c_void_p(k.data_ptr()), ctypes.c_void_p(v.data_ptr()),
+                ctypes.c_void_p(o.data_ptr()), batch, heads, lq, lk, ctypes.c_float(0.125))
+        for _ in range(3):
+            assert lib.dmx_op_attention(*args) == 0, lib.dmx_last_error()
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record(stream)
+        for _ in range(iters):
+            lib.dmx_op_attention(*args)
+        end.record(stream)
+        end.synchronize()
+        ms = start.elapsed_time(end) / iters
+        flops = 4.0 * batch * lq * lk * D  # QK^T + PV, 2 flops per MAC
+        results.append((ms, flops))
+    ms = sum(r[0] for r in results) / len(results)
+    flops = sum(r[1] for r in results) / len(results)
+    return ms, flops
+
+
+def cpu_baseline(pkg, seconds_budget: float = 20.0):
+    """The restated reference CPU backend on one 7.8 s segment (config 1):
+    1 warm-up, then the median of up to 3 timed forwards within the budget."""
+    sys.path.insert(0, str(ROOT))
+    from oracle import binding as oracle
+    cfg = pkg.Config()
+    weights = pkg.random_init(0, cfg)
+    mix = pkg.signals.gaussian_segments(0, 1, cfg.training_length)
+    model = oracle.Model(weights, cfg)
+    t0 = time.perf_counter()
+    model.forward(mix)
+    first = time.perf_counter() - t0
+    times = []
+    while len(times) < 3 and (sum(times) + first) < seconds_budget:
+        t0 = time.perf_counter()
+        model.forward(mix)
+        times.append(time.perf_counter() - t0)
+    t = float(np.median(times)) if times else first
+    seg_s = cfg.training_length / cfg.samplerate
+    return {"value": round(seg_s / t, 4), "unit": "x-realtime", "cores": oracle.threads(), "kind": "port",
+            "sample": f"one {seg_s:.1f} s segment forward (config 1), median of {max(1, len(times))} after 1 warm-up; "
+                      f"{t:.2f} s per forward"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=5)
+    ap.add_argument("--warmup", type=int, default=1)
+    ap.add_argument("--seconds", type=float, default=60.0, help="mix length")
+    ap.add_argument("--batch-chunks", type=int, default=8)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--attn-iters", type=int, default=20)
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py: this build runs on one GPU only; multi-GPU runs are not part of it "
+              "(the path would shard by chunk ranges, see DESIGN.md)", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    pkg = load_package()
+    cfg = pkg.Config()
+    weights = pkg.random_init(0, cfg)
+    runner = pkg.Runner(weights, cfg, device=0)
+    mix = pkg.signals.synthetic_mix(0, args.seconds)
+    samples = mix.shape[1]
+    d_mix = torch.from_numpy(mix).cuda()
+    d_stems = torch.empty((cfg.sources, 2, samples), device="cuda")
+    opts = pkg.SeparateOptions(shifts=0, overlap=0.25, batch_chunks=args.batch_chunks).to_c()
+    lib = pkg._native.load()
+    handles = (ctypes.c_void_p * 1)(runner.handle)
+
+    def step():
+        rc = lib.dmx_separate_device(handles, None, 1, None, ctypes.c_void_p(d_mix.data_ptr()), samples,
+                                     cfg.samplerate, ctypes.byref(opts), pkg._native.PROGRESS(), None,
+                                     ctypes.c_void_p(d_stems.data_ptr()))
+        if rc != 0:
+            raise RuntimeError(pkg._native.last_error())
+
+    for _ in range(args.warmup):
+        step()
+    runner.synchronize()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    runner.synchronize()
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    ms_per_step = 1000.0 * elapsed / args.steps
+    audio_s = samples / cfg.samplerate
+    xrt = audio_s * args.steps / elapsed
+    if not np.isfinite(d_stems.abs().sum().item()):
+        raise RuntimeError("non-finite stems")
+
+    attn_ms, attn_flops = attention_roofline(pkg, torch, args.batch_chunks, args.attn_iters)
+    attn_tflops = attn_flops / (attn_ms * 1e-3) / 1e12
+    roofline = {"bound": "mfma", "achieved": round(attn_tflops, 2), "peak": FP32_MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
+                "frac": round(attn_tflops / FP32_MFMA_PEAK_TFLOPS, 4), "traffic": None,
+                "kernel": "attention_kernel (fused cross-attention, fp32 MFMA)",
+                "per_launch": f"4*B*Lq*Lk*512 flops, B={args.batch_chunks}, (Lq, Lk) = (2688, 1344) and (1344, 2688); "
+                              f"avg {attn_ms:.3f} ms per launch"}
+    line = {
+        "metric": "htdemucs x-realtime (audio s / wall s) on 1 MI355X; cross-attn TFLOP/s",
+        "value": round(xrt, 2),
+        "unit": "x-realtime",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 2),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (seeded 60 s mix: 16 sinusoids + pink noise + decaying bursts; random-init seed-0 weights)",
+        "config": {"workload": f"config 3: htdemucs separation of a {args.seconds:g} s stereo mix, 7.8 s segments, "
+                               f"overlap 0.25, {args.batch_chunks} chunks per launch, shifts=0, fp32, "
+                               "mix and stems resident in HBM",
+                   "segment_samples": cfg.training_length, "batch_chunks": args.batch_chunks},
+        "cross_attn_tflops": round(attn_tflops, 2),
+        "roofline": roofline,
+        "cpu_baseline": None if args.no_cpu_baseline else cpu_baseline(pkg),
+    }
+    print(json.dumps(line))
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,153 @@
+// capi_ops.hip — include/dmx_ops.h: one kernel (group) per call, on the
+// caller's stream, for the parity tests.
+#include <hip/hip_runtime.h>
+
+#include <vector>
+
+#include "../../include/dmx_ops.h"
+#include "common.h"
+#include "ops.h"
+
+using namespace dmx;
+
+namespace {
+
+hipStream_t as_stream(void *s) { return static_cast<hipStream_t>(s); }
+
+// Twiddles + window for nfft 4096, uploaded once per process (per device 0 context).
+const float *twiddles_4096() {
+    static float *d = nullptr;
+    if (!d) {
+        std::vector<float> h(4096 / 2 * 2 + 4096);
+        make_twiddles(4096, h.data());
+        DMX_HIP(hipMalloc(&d, h.size() * sizeof(float)));
+        DMX_HIP(hipMemcpy(d, h.data(), h.size() * sizeof(float), hipMemcpyHostToDevice));
+    }
+    return d;
+}
+
+struct Scratch {
+    void *p = nullptr;
+    explicit Scratch(size_t bytes) { DMX_HIP(hipMalloc(&p, std::max<size_t>(bytes, 16))); }
+    ~Scratch() { (void)hipFree(p); }
+};
+
+}  // namespace
+
+extern "C" {
+
+int dmx_op_conv2d(void *stream, const float *x, const float *skip, int b, int ic, int h, int w, const float *weight,
+                  const float *bias, int oc, int kh, int kw, int sh, int sw, int ph, int pw, int dh, int dw, int act,
+                  float *out) {
+    return guarded([&] {
+        conv2d(as_stream(stream), x, skip, b, ic, h, w, weight, bias, oc, kh, kw, sh, sw, ph, pw, dh, dw, out,
+               (Act)act);
+    });
+}
+
+int dmx_op_conv2d_glu(void *stream, const float *x, const float *skip, int b, int ic, int h, int w,
+                      const float *weight, const float *bias, int C, int kh, int kw, int ph, int pw, const float *emb,
+                      float emb_scale, float *out) {
+    return guarded([&] {
+        conv2d_glu(as_stream(stream), x, skip, b, ic, h, w, weight, bias, C, kh, kw, ph, pw, out, emb, emb_scale);
+    });
+}
+
+int dmx_op_conv_transpose(void *stream, const float *x, int b, int ic, int A, int P, const float *weight,
+                          const float *bias, int oc, int k, int st, int crop, int a_out, int act, float *out) {
+    return guarded([&] {
+        hipStream_t s = as_stream(stream);
+        std::vector<float> hw((size_t)ic * oc * k);
+        DMX_HIP(hipStreamSynchronize(s));
+        DMX_HIP(hipMemcpy(hw.data(), weight, hw.size() * sizeof(float), hipMemcpyDeviceToHost));
+        int taps = conv_transpose_taps(k, st);
+        std::vector<float> packed((size_t)st * oc * ic * taps);
+        pack_conv_transpose(hw.data(), ic, oc, k, st, packed.data());
+        Scratch d(packed.size() * sizeof(float));
+        DMX_HIP(hipMemcpy(d.p, packed.data(), packed.size() * sizeof(float), hipMemcpyHostToDevice));
+        conv_transpose_axis(s, x, b, ic, A, P, static_cast<float *>(d.p), bias, oc, k, st, crop, a_out, out,
+                            (Act)act);
+        DMX_HIP(hipStreamSynchronize(s));
+    });
+}
+
+int dmx_op_dconv_layer(void *stream, float *x, int B, int C, int F, int T, int dilation, const float *w1,
+                       const float *b1, int hidden, const float *n1w, const float *n1b, const float *w2,
+                       const float *b2, const float *n2w, const float *n2b, const float *gamma) {
+    return guarded([&] {
+        hipStream_t s = as_stream(stream);
+        Scratch h((size_t)B * F * hidden * T * sizeof(float)), st((size_t)4 * B * F * sizeof(double));
+        dconv_layer(s, x, B, C, F, T, dilation, w1, b1, hidden, n1w, n1b, w2, b2, n2w, n2b, gamma,
+                    static_cast<float *>(h.p), static_cast<double *>(st.p));
+        DMX_HIP(hipStreamSynchronize(s));
+    });
+}
+
+int dmx_op_linear(void *stream, const float *x, int rows, int K, const float *w, const float *bias, int N, int tail,
+                  const float *residual, const float *gamma, float *out) {
+    return guarded([&] {
+        linear(as_stream(stream), x, K, (int64_t)rows * K, w, bias, 1, rows, K, N, out, N, (int64_t)rows * N,
+               (LinearTail)tail, residual, gamma, nullptr);
+    });
+}
+
+int dmx_op_pointwise(void *stream, const float *w, const float *bias, const float *x, int batches, int M, int K,
+                     int N, float *out) {
+    return guarded([&] { pointwise(as_stream(stream), w, bias, x, batches, M, K, N, out, ACT_NONE); });
+}
+
+int dmx_op_attention(void *stream, const float *q, const float *k, const float *v, float *out, int batch, int heads,
+                     int n_q, int n_k, float scale) {
+    return guarded([&] {
+        int64_t D = (int64_t)heads * 64;
+        attention(as_stream(stream), q, D, k, D, v, D, out, D, batch, heads, n_q, n_k, 64, scale, n_q * D, n_k * D,
+                  n_q * D);
+    });
+}
+
+int dmx_op_layer_norm(void *stream, const float *x, int rows, int dim, const float *w, const float *b, float *out) {
+    return guarded([&] { layer_norm_rows(as_stream(stream), x, rows, dim, w, b, out, nullptr, 0); });
+}
+
+int dmx_op_group_norm(void *stream, const float *x, int b, int c, int inner, int groups, const float *w,
+                      const float *bias, float *out) {
+    return guarded([&] {
+        hipStream_t s = as_stream(stream);
+        Scratch st((size_t)2 * b * groups * sizeof(double));
+        group_norm(s, x, b, c, inner, groups, w, bias, out, static_cast<double *>(st.p));
+        DMX_HIP(hipStreamSynchronize(s));
+    });
+}
+
+int dmx_op_glu(void *stream, const float *x, int b, int c2, int inner, float *out) {
+    return guarded([&] { glu(as_stream(stream), x, b, c2, inner, out); });
+}
+
+int dmx_op_gelu(void *stream, const float *x, int64_t n, float *out) {
+    return guarded([&] { gelu(as_stream(stream), x, n, out); });
+}
+
+int dmx_op_spec_normalise(void *stream, const float *mix, int b, int L, float *xspec, float *xwave, float *norms) {
+    return guarded([&] {
+        hipStream_t s = as_stream(stream);
+        int le = (L + 1023) / 1024;
+        Scratch frames((size_t)b * 2 * le * 2048 * 2 * sizeof(float)), st((size_t)4 * b * sizeof(double));
+        spec_and_normalise(s, mix, b, L, 4096, static_cast<float *>(frames.p), xspec, xwave, norms,
+                           static_cast<double *>(st.p), twiddles_4096());
+        DMX_HIP(hipStreamSynchronize(s));
+    });
+}
+
+int dmx_op_ispec_sum(void *stream, const float *xspec, const float *xtime, int b, int L, const float *norms,
+                     float *stems) {
+    return guarded([&] {
+        hipStream_t s = as_stream(stream);
+        int le = (L + 1023) / 1024, rows = b * 8;
+        Scratch scratch(((size_t)rows * le * 4096 + (size_t)rows * le * 2048 * 2) * sizeof(float));
+        ispec_and_sum(s, xspec, xtime, b, 4, L, 4096, le, norms, static_cast<float *>(scratch.p), stems,
+                      twiddles_4096());
+        DMX_HIP(hipStreamSynchronize(s));
+    });
+}
+
+}  // extern "C"

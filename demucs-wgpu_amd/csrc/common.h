@@ -1,0 +1,147 @@
+// common.h — shared host/device helpers for the HIP backend (gfx950 only).
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <cstdio>
+#include <stdexcept>
+#include <string>
+
+namespace dmx {
+
+// Error carrying one of the dmx_status codes of include/dmx.h.
+struct Error : std::runtime_error {
+    int code;
+    Error(int c, const std::string &msg) : std::runtime_error(msg), code(c) {}
+};
+
+[[noreturn]] inline void throw_error(int code, const std::string &msg) { throw Error(code, msg); }
+
+#define DMX_HIP(expr)                                                                             \
+    do {                                                                                          \
+        hipError_t _e = (expr);                                                                   \
+        if (_e != hipSuccess)                                                                     \
+            ::dmx::throw_error(6, std::string(#expr) + " failed: " + hipGetErrorString(_e) +      \
+                                      " (" + __FILE__ + ":" + std::to_string(__LINE__) + ")");  \
+    } while (0)
+
+#define DMX_LAUNCH_CHECK() DMX_HIP(hipGetLastError())
+
+#define DMX_REQUIRE(cond, msg)                                                                    \
+    do {                                                                                          \
+        if (!(cond)) ::dmx::throw_error(1, std::string(msg));                                     \
+    } while (0)
+
+inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+// Host-side check that every operand a kernel will dereference is non-null,
+// so a wiring mistake is an error at the launch instead of a device fault.
+inline void require_ptrs(std::initializer_list<const void *> ptrs, const char *what) {
+    for (const void *p : ptrs)
+        if (!p) throw Error(8, std::string(what) + ": null device pointer");
+}
+
+// The calling thread's last error message (dmx_last_error).
+std::string &last_error_slot();
+
+// Runs f, turning exceptions into a dmx_status code and a message.
+template <class F>
+int guarded(F &&f) {
+    try {
+        f();
+        last_error_slot().clear();
+        return 0;
+    } catch (const Error &e) {
+        last_error_slot() = e.what();
+        return e.code;
+    } catch (const std::bad_alloc &) {
+        last_error_slot() = "out of host memory";
+        return 7;
+    } catch (const std::exception &e) {
+        last_error_slot() = e.what();
+        return 6;
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Device math shared by every kernel.
+// ---------------------------------------------------------------------------
+
+// erf via the Numerical Recipes rational approximation of erfc (Press et al.,
+// "erfcc", fractional error < 1.2e-7) — the same published formula the
+// reference's CPU GELU uses (crates/demucs-core/src/ops.rs:101-121), so the
+// device matches it to the rounding of the exponential.
+__device__ __forceinline__ float erf_nr(float x) {
+    float z = fabsf(x);
+    float t = 1.0f / (1.0f + 0.5f * z);
+    float poly =
+        -z * z - 1.26551223f +
+        t * (1.00002368f +
+             t * (0.37409196f +
+                  t * (0.09678418f +
+                       t * (-0.18628806f +
+                            t * (0.27886807f +
+                                 t * (-1.13520398f +
+                                      t * (1.48851587f + t * (-0.82215223f + t * 0.17087277f))))))));
+    float tau = t * expf(poly);
+    float value = 1.0f - tau;
+    return x >= 0.0f ? value : -value;
+}
+
+// Exact (erf) GELU: 0.5 x (1 + erf(x / sqrt 2)).
+__device__ __forceinline__ float gelu(float x) { return 0.5f * x * (1.0f + erf_nr(x * 0.70710678118654752440f)); }
+
+__device__ __forceinline__ float sigmoid(float g) { return 1.0f / (1.0f + expf(-g)); }
+
+// Wave64 reductions.
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    return v;
+}
+__device__ __forceinline__ double wave_sum_d(double v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    return v;
+}
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+    return v;
+}
+
+// Block-wide f64 (sum, sum of squares) reduction, then one atomic add per block
+// into dst[0], dst[1]. blockDim.x must be a multiple of 64 and <= 1024.
+__device__ inline void block_moments_atomic(double s, double q, double *dst) {
+    __shared__ double red_s[16], red_q[16];
+    s = wave_sum_d(s);
+    q = wave_sum_d(q);
+    int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, waves = blockDim.x >> 6;
+    if (lane == 0) {
+        red_s[wave] = s;
+        red_q[wave] = q;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        double ts = 0.0, tq = 0.0;
+        for (int w = 0; w < waves; ++w) {
+            ts += red_s[w];
+            tq += red_q[w];
+        }
+        atomicAdd(dst, ts);
+        atomicAdd(dst + 1, tq);
+    }
+}
+
+// GroupNorm(1) statistics from (sum, sum of squares) in f64, as the reference
+// turns them into f32 (crates/demucs-core/src/demucs/ops.rs:568-579):
+// mean = s/n, var = max(q/n - mean^2, 0), inv = 1 / (float)sqrt(var + 1e-5).
+__device__ __forceinline__ void gn_stats(const double *sq, double count, float &mean, float &inv) {
+    double m = sq[0] / count;
+    double var = fmax(sq[1] / count - m * m, 0.0);
+    mean = (float)m;
+    inv = 1.0f / (float)sqrt(var + 1e-5);
+}
+
+}  // namespace dmx

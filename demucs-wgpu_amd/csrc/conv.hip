@@ -1,0 +1,519 @@
+// conv.hip — every GEMM-shaped op of the forward, as loaders + epilogues over
+// the MFMA GEMM of gemm.h: implicit-GEMM convolutions (nothing im2col'd to
+// HBM), GLU-fused rewrites, transposed convolutions as per-phase GEMMs, the
+// fused DConv layer, channel mixers and the transformer linears.
+#include "gemm.h"
+#include "ops.h"
+
+namespace dmx {
+namespace {
+
+// ---------------------------------------------------------------------------
+// Loaders
+// ---------------------------------------------------------------------------
+
+// Implicit im2col of nn.Conv2d (crates/demucs-core/src/demucs/ops.rs:44-211):
+// B[k][n] with k = (ic, ky, kx), n = (oy, ox); zero outside the input.
+// The z-th problem's input starts at (z / zdiv) * outer + (z % zdiv) * inner,
+// which lets a DConv treat the (b, f) rows of a (B, C, F, T) tensor as its
+// batch without a permute. KH/KW > 0 fix the kernel at compile time.
+template <int KH, int KW>
+struct ConvGather {
+    static constexpr bool kmajor = false;
+    const float *x, *skip;
+    int64_t outer, inner, cs;  // batch strides and channel stride
+    int zdiv, h, w, kh_rt, kw_rt, sh, sw, ph, pw, dh, dw, ow;
+    struct State {
+        const float *base;
+        const float *sbase;
+        int iy0, ix0;
+    };
+    __device__ int kh() const { return KH > 0 ? KH : kh_rt; }
+    __device__ int kw() const { return KW > 0 ? KW : kw_rt; }
+    __device__ State setup(int z, int n) const {
+        int oy = n / ow, ox = n - oy * ow;
+        int64_t off = (int64_t)(z / zdiv) * outer + (int64_t)(z % zdiv) * inner;
+        return {x + off, skip ? skip + off : nullptr, oy * sh - ph, ox * sw - pw};
+    }
+    __device__ float load(const State &s, int k) const {
+        const int taps = kh() * kw();
+        int c = k / taps, tap = k - c * taps;
+        int ky = tap / kw(), kx = tap - ky * kw();
+        int iy = s.iy0 + ky * dh, ix = s.ix0 + kx * dw;
+        if (iy < 0 || iy >= h || ix < 0 || ix >= w) return 0.0f;
+        int64_t at = c * cs + (int64_t)iy * w + ix;
+        float v = s.base[at];
+        if (s.sbase) v += s.sbase[at];
+        return v;
+    }
+};
+
+// DConv conv2's input: GroupNorm(1) + GELU of conv1's output, applied while
+// loading. y is (rows, H, T); stats holds (sum, sum_sq) per row.
+struct NormGeluRows {
+    static constexpr bool kmajor = false;
+    const float *y;
+    const double *stats;
+    const float *nw, *nb;
+    int H, T;
+    struct State {
+        const float *col;
+        float mean, inv;
+    };
+    __device__ State setup(int z, int n) const {
+        float mean, inv;
+        gn_stats(stats + 2 * z, (double)H * (double)T, mean, inv);
+        return {y + (int64_t)z * H * T + n, mean, inv};
+    }
+    __device__ float load(const State &s, int k) const {
+        float scale = s.inv * nw[k];
+        float shift = nb[k] - s.mean * scale;
+        return gelu(s.col[(int64_t)k * T] * scale + shift);
+    }
+};
+
+// Transposed convolution along one axis, one output phase per problem:
+// z = b * st + p; output positions a' = st*q + p - crop with q = qmin(p) + n / P.
+// Tap j of input row q - j meets kernel index p + st*j.
+template <int TAPS>
+struct ConvTGather {
+    static constexpr bool kmajor = false;
+    const float *x;
+    int ic, A, P, st, crop;
+    struct State {
+        const float *base;
+        int q;
+    };
+    __device__ State setup(int z, int n) const {
+        int b = z / st, p = z - b * st;
+        int qmin = crop > p ? (crop - p + st - 1) / st : 0;
+        int qi = n / P, t = n - qi * P;
+        return {x + (int64_t)b * ic * A * P + t, qmin + qi};
+    }
+    __device__ float load(const State &s, int k) const {
+        int c = k / TAPS, j = k - c * TAPS;
+        int a = s.q - j;
+        if (a < 0 || a >= A) return 0.0f;
+        return s.base[((int64_t)c * A + a) * P];
+    }
+};
+
+// Phase-packed transposed-conv weights: (st, oc, ic*taps), k-major rows.
+struct PhaseWeights {
+    static constexpr bool kmajor = true;
+    const float *w;
+    int st, oc, K;
+    bool vec;
+    struct State {
+        const float *row;
+    };
+    __device__ State setup(int z, int m) const { return {w + ((int64_t)(z % st) * oc + m) * K}; }
+    __device__ float4 load4(const State &s, int k, int Kt) const {
+        if (vec && k + 3 < Kt) return *reinterpret_cast<const float4 *>(s.row + k);
+        float4 v;
+        v.x = k < Kt ? s.row[k] : 0.f;
+        v.y = k + 1 < Kt ? s.row[k + 1] : 0.f;
+        v.z = k + 2 < Kt ? s.row[k + 2] : 0.f;
+        v.w = k + 3 < Kt ? s.row[k + 3] : 0.f;
+        return v;
+    }
+};
+
+// Transformer tokens (b, T*F, D) read as a (D, F*T) channel-major operand:
+// column n = f*T + t is token t*F + f.
+struct TokenGather {
+    static constexpr bool kmajor = true;
+    const float *tok;
+    int F, T, D;
+    struct State {
+        const float *row;
+    };
+    __device__ State setup(int z, int n) const {
+        int f = n / T, t = n - f * T;
+        return {tok + ((int64_t)z * F * T + (int64_t)t * F + f) * D};
+    }
+    __device__ float4 load4(const State &s, int k, int K) const {
+        if (k + 3 < K) return *reinterpret_cast<const float4 *>(s.row + k);
+        float4 v;
+        v.x = k < K ? s.row[k] : 0.f;
+        v.y = k + 1 < K ? s.row[k + 1] : 0.f;
+        v.z = k + 2 < K ? s.row[k + 2] : 0.f;
+        v.w = k + 3 < K ? s.row[k + 3] : 0.f;
+        return v;
+    }
+};
+
+// ---------------------------------------------------------------------------
+// Epilogues
+// ---------------------------------------------------------------------------
+
+__device__ __forceinline__ float act_apply(int act, float v) { return act == ACT_GELU ? gelu(v) : v; }
+
+// out[z][m][n] = act(v + bias[m]), row length N.
+struct EpChannels : EpBase {
+    float *out;
+    const float *bias;
+    int64_t batch_stride;
+    int N, act;
+    __device__ void store(int z, int m, int n, float v) {
+        float b = bias ? bias[m] : 0.0f;
+        out[z * batch_stride + (int64_t)m * N + n] = act_apply(act, v + b);
+    }
+};
+
+// GLU over channel pairs (c, C + c), plus the optional frequency embedding.
+struct EpGlu : EpBase {
+    float *out;
+    const float *bias;
+    const float *emb;  // (F, C) already scaled by emb_scale
+    float emb_scale;
+    int64_t batch_stride;
+    int N, C, T;
+    __device__ void glu(int z, int c, int n, float v, float g) {
+        float a = v + bias[c], gate = g + bias[C + c];
+        float y = a * sigmoid(gate);
+        if (emb) y += emb_scale * emb[(n / T) * C + c];
+        out[z * batch_stride + (int64_t)c * N + n] = y;
+    }
+};
+
+// Transposed-conv output: scatter phase rows back into the cropped axis.
+struct EpConvT : EpBase {
+    float *out;
+    const float *bias;
+    int oc, st, crop, a_out, P, act;
+    __device__ void store(int z, int m, int n, float v) {
+        int b = z / st, p = z - b * st;
+        int qmin = crop > p ? (crop - p + st - 1) / st : 0;
+        int qi = n / P, t = n - qi * P;
+        int a = st * (qmin + qi) + p - crop;
+        if (a >= a_out) return;
+        out[(((int64_t)b * oc + m) * a_out + a) * P + t] = act_apply(act, v + bias[m]);
+    }
+};
+
+// DConv conv1: y = conv + bias stored as (rows, H, T); GN statistics per row.
+struct EpConv1 {
+    float *y;
+    const float *bias;
+    double *stats;
+    int H, T;
+    MomentAcc acc;
+    __device__ void init(int) {}
+    __device__ void store(int z, int m, int n, float v) {
+        float r = v + bias[m];
+        y[((int64_t)z * H + m) * T + n] = r;
+        acc.add(r);
+    }
+    __device__ void finalize(int z) { acc.flush(stats + 2 * z); }
+};
+
+// DConv conv2, first pass: GN statistics of (conv + bias), nothing stored.
+struct EpConv2Stats {
+    const float *bias;
+    double *stats;
+    MomentAcc acc;
+    __device__ void init(int) {}
+    __device__ void store(int, int m, int, float v) { acc.add(v + bias[m]); }
+    __device__ void finalize(int z) { acc.flush(stats + 2 * z); }
+};
+
+// DConv conv2, second pass: GN -> GLU -> LayerScale -> residual add into x,
+// whose rows (b, f) live in a (B, C, F, T) tensor.
+struct EpConv2Apply {
+    float *x;
+    const float *bias, *nw, *nb, *gamma;
+    const double *stats;
+    int C, F, T;
+    float mean, inv;
+    __device__ void init(int z) { gn_stats(stats + 2 * z, 2.0 * C * (double)T, mean, inv); }
+    __device__ void glu(int z, int c, int n, float v, float g) {
+        float vs = inv * nw[c], vsh = nb[c] - mean * vs;
+        float gs = inv * nw[C + c], gsh = nb[C + c] - mean * gs;
+        float value = (v + bias[c]) * vs + vsh;
+        float gate = (g + bias[C + c]) * gs + gsh;
+        int b = z / F, f = z - b * F;
+        float *dst = x + (((int64_t)b * C + c) * F + f) * T + n;
+        *dst += gamma[c] * (value * sigmoid(gate));
+    }
+    __device__ void finalize(int) {}
+};
+
+// Linear tails on token rows.
+struct EpLinear {
+    float *out;
+    const float *bias, *residual, *gamma;
+    double *stats;
+    int64_t ldo, batch_stride;
+    int tail;
+    MomentAcc acc;
+    __device__ void init(int) {}
+    __device__ void store(int z, int m, int n, float v) {
+        int64_t at = z * batch_stride + (int64_t)m * ldo + n;
+        float a = v + bias[n];
+        if (tail == TAIL_BIAS_GELU) {
+            a = gelu(a);
+        } else if (tail == TAIL_RESIDUAL_SCALE) {
+            a = residual[at] + a * gamma[n];
+            if (stats) acc.add(a);
+        }
+        out[at] = a;
+    }
+    __device__ void finalize(int z) {
+        if (stats) acc.flush(stats + 2 * z);
+    }
+};
+
+// ---------------------------------------------------------------------------
+// Tile selection
+// ---------------------------------------------------------------------------
+
+template <bool GLU, class AL, class BL, class EP>
+void gemm_auto(hipStream_t s, int M, int N, int K, int batches, const AL &al, const BL &bl, const EP &ep) {
+    if constexpr (GLU) {
+        if (M > 32)
+            launch_gemm<128, 128, 2, true>(s, M, N, K, batches, al, bl, ep);
+        else
+            launch_gemm<64, 128, 1, true>(s, M, N, K, batches, al, bl, ep);
+    } else {
+        if (M >= 96)
+            launch_gemm<128, 128, 2, false>(s, M, N, K, batches, al, bl, ep);
+        else if (M > 32)
+            launch_gemm<64, 128, 2, false>(s, M, N, K, batches, al, bl, ep);
+        else
+            launch_gemm<32, 256, 1, false>(s, M, N, K, batches, al, bl, ep);
+    }
+}
+
+bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+
+KMajor kmajor(const float *p, int64_t ld, int64_t batch_stride) {
+    return KMajor{p, ld, batch_stride, aligned16(p) && ld % 4 == 0 && batch_stride % 4 == 0};
+}
+
+template <int KH, int KW>
+ConvGather<KH, KW> gather(const float *x, const float *skip, int64_t outer, int64_t inner, int zdiv, int ic_stride_h,
+                          int h, int w, int kh, int kw, int sh, int sw, int ph, int pw, int dh, int dw, int ow) {
+    ConvGather<KH, KW> g;
+    g.x = x;
+    g.skip = skip;
+    g.outer = outer;
+    g.inner = inner;
+    g.cs = (int64_t)ic_stride_h * w;
+    g.zdiv = zdiv;
+    g.h = h;
+    g.w = w;
+    g.kh_rt = kh;
+    g.kw_rt = kw;
+    g.sh = sh;
+    g.sw = sw;
+    g.ph = ph;
+    g.pw = pw;
+    g.dh = dh;
+    g.dw = dw;
+    g.ow = ow;
+    return g;
+}
+
+// Runs a conv GEMM with a compile-time kernel when it is one of the model's.
+template <bool GLU, class EP>
+void conv_dispatch(hipStream_t s, int M, int N, int K, int batches, const KMajor &wa, const float *x,
+                   const float *skip, int64_t outer, int64_t inner, int zdiv, int ic_stride_h, int h, int w, int kh,
+                   int kw, int sh, int sw, int ph, int pw, int dh, int dw, int ow, const EP &ep) {
+    require_ptrs({x, wa.p}, "conv");
+#define DMX_CONV_CASE(A, B)                                                                                \
+    if (kh == A && kw == B) {                                                                                \
+        gemm_auto<GLU>(s, M, N, K, batches, wa,                                                              \
+                       gather<A, B>(x, skip, outer, inner, zdiv, ic_stride_h, h, w, kh, kw, sh, sw, ph, pw, dh, \
+                                    dw, ow),                                                                 \
+                       ep);                                                                                  \
+        return;                                                                                              \
+    }
+    DMX_CONV_CASE(8, 1)
+    DMX_CONV_CASE(1, 8)
+    DMX_CONV_CASE(3, 3)
+    DMX_CONV_CASE(1, 3)
+    DMX_CONV_CASE(1, 1)
+#undef DMX_CONV_CASE
+    gemm_auto<GLU>(s, M, N, K, batches, wa,
+                   gather<0, 0>(x, skip, outer, inner, zdiv, ic_stride_h, h, w, kh, kw, sh, sw, ph, pw, dh, dw, ow), ep);
+}
+
+}  // namespace
+
+// ---------------------------------------------------------------------------
+// Launchers
+// ---------------------------------------------------------------------------
+
+void conv2d(hipStream_t s, const float *x, const float *skip, int b, int ic, int h, int w, const float *weight,
+            const float *bias, int oc, int kh, int kw, int sh, int sw, int ph, int pw, int dh, int dw, float *out,
+            Act act) {
+    int eh = dh * (kh - 1) + 1, ew = dw * (kw - 1) + 1;
+    DMX_REQUIRE(h + 2 * ph >= eh && w + 2 * pw >= ew, "conv2d: kernel larger than the padded input");
+    int oh = (h + 2 * ph - eh) / sh + 1, ow = (w + 2 * pw - ew) / sw + 1;
+    int K = ic * kh * kw, N = oh * ow;
+    EpChannels ep;
+    ep.out = out;
+    ep.bias = bias;
+    ep.batch_stride = (int64_t)oc * N;
+    ep.N = N;
+    ep.act = act;
+    conv_dispatch<false>(s, oc, N, K, b, kmajor(weight, K, 0), x, skip, (int64_t)ic * h * w, 0, 1, h, h, w, kh, kw, sh,
+                         sw, ph, pw, dh, dw, ow, ep);
+}
+
+void conv1d_right_padded(hipStream_t s, const float *x, int b, int ic, int len, int len_padded, const float *weight,
+                         const float *bias, int oc, int k, int stride, int pad, float *out, Act act) {
+    DMX_REQUIRE(len_padded >= len && len_padded + 2 * pad >= k, "conv1d_right_padded: bad lengths");
+    int ow = (len_padded + 2 * pad - k) / stride + 1;
+    int K = ic * k;
+    EpChannels ep;
+    ep.out = out;
+    ep.bias = bias;
+    ep.batch_stride = (int64_t)oc * ow;
+    ep.N = ow;
+    ep.act = act;
+    // Bounds use the unpadded length: the right pad is zeros either way.
+    conv_dispatch<false>(s, oc, ow, K, b, kmajor(weight, K, 0), x, nullptr, (int64_t)ic * len, 0, 1, 1, 1, len, 1, k, 1,
+                         stride, 0, pad, 1, 1, ow, ep);
+}
+
+void conv2d_glu(hipStream_t s, const float *x, const float *skip, int b, int ic, int h, int w, const float *weight,
+                const float *bias, int C, int kh, int kw, int ph, int pw, float *out, const float *emb,
+                float emb_scale) {
+    require_ptrs({bias, out}, "conv2d_glu");
+    int oh = h + 2 * ph - kh + 1, ow = w + 2 * pw - kw + 1;
+    DMX_REQUIRE(oh > 0 && ow > 0, "conv2d_glu: kernel larger than the padded input");
+    int K = ic * kh * kw, N = oh * ow;
+    EpGlu ep;
+    ep.out = out;
+    ep.bias = bias;
+    ep.emb = emb;
+    ep.emb_scale = emb_scale;
+    ep.batch_stride = (int64_t)C * N;
+    ep.N = N;
+    ep.C = C;
+    ep.T = ow;
+    conv_dispatch<true>(s, C, N, K, b, kmajor(weight, K, 0), x, skip, (int64_t)ic * h * w, 0, 1, h, h, w, kh, kw, 1, 1,
+                        ph, pw, 1, 1, ow, ep);
+}
+
+int conv_transpose_taps(int k, int st) { return (k + st - 1) / st; }
+
+void pack_conv_transpose(const float *w, int ic, int oc, int k, int st, float *packed) {
+    int taps = conv_transpose_taps(k, st);
+    for (int p = 0; p < st; ++p)
+        for (int o = 0; o < oc; ++o)
+            for (int c = 0; c < ic; ++c)
+                for (int j = 0; j < taps; ++j) {
+                    int kk = p + st * j;
+                    packed[((int64_t)(p * oc + o) * ic + c) * taps + j] = kk < k ? w[((int64_t)c * oc + o) * k + kk] : 0.0f;
+                }
+}
+
+void conv_transpose_axis(hipStream_t s, const float *x, int b, int ic, int A, int P, const float *weight_packed,
+                         const float *bias, int oc, int k, int st, int crop, int a_out, float *out, Act act) {
+    require_ptrs({x, weight_packed, bias, out}, "conv_transpose_axis");
+    int taps = conv_transpose_taps(k, st);
+    DMX_REQUIRE(taps == 2, "conv_transpose_axis: only kernel = 2 * stride is supported");
+    DMX_REQUIRE(crop + a_out <= (A - 1) * st + k, "conv_transpose_axis: crop past the produced length");
+    int max_count = 0;
+    for (int p = 0; p < st; ++p) {
+        int qmin = crop > p ? (crop - p + st - 1) / st : 0;
+        int qend = (a_out + crop - p + st - 1) / st;
+        max_count = std::max(max_count, qend - qmin);
+    }
+    int K = ic * taps, N = max_count * P;
+    ConvTGather<2> g{x, ic, A, P, st, crop};
+    PhaseWeights pw{weight_packed, st, oc, K, aligned16(weight_packed) && K % 4 == 0};
+    EpConvT ep;
+    ep.out = out;
+    ep.bias = bias;
+    ep.oc = oc;
+    ep.st = st;
+    ep.crop = crop;
+    ep.a_out = a_out;
+    ep.P = P;
+    ep.act = act;
+    gemm_auto<false>(s, oc, N, K, b * st, pw, g, ep);
+}
+
+void dconv_layer(hipStream_t s, float *x, int B, int C, int F, int T, int dil, const float *w1, const float *b1,
+                 int H, const float *n1w, const float *n1b, const float *w2, const float *b2, const float *n2w,
+                 const float *n2b, const float *gamma, float *hbuf, double *stats) {
+    require_ptrs({x, w1, b1, n1w, n1b, w2, b2, n2w, n2b, gamma, hbuf, stats}, "dconv_layer");
+    const int rows = B * F;
+    DMX_REQUIRE(rows <= 65535, "dconv_layer: too many rows for one launch");
+    double *st1 = stats, *st2 = stats + 2 * rows;
+    zero_doubles(s, stats, 4 * (int64_t)rows);
+    // conv1: k3, dilation dil, padding dil, over t; rows (b, f) as the batch.
+    EpConv1 e1;
+    e1.y = hbuf;
+    e1.bias = b1;
+    e1.stats = st1;
+    e1.H = H;
+    e1.T = T;
+    conv_dispatch<false>(s, H, T, C * 3, rows, kmajor(w1, C * 3, 0), x, nullptr, (int64_t)C * F * T, T, F, F, 1, T, 1, 3,
+                         1, 1, 0, dil, 1, dil, T, e1);
+    // conv2 (1x1 over H) twice: statistics, then GN + GLU + LayerScale + residual.
+    NormGeluRows ng{hbuf, st1, n1w, n1b, H, T};
+    EpConv2Stats e2;
+    e2.bias = b2;
+    e2.stats = st2;
+    gemm_auto<false>(s, 2 * C, T, H, rows, kmajor(w2, H, 0), ng, e2);
+    EpConv2Apply e3;
+    e3.x = x;
+    e3.bias = b2;
+    e3.nw = n2w;
+    e3.nb = n2b;
+    e3.gamma = gamma;
+    e3.stats = st2;
+    e3.C = C;
+    e3.F = F;
+    e3.T = T;
+    gemm_auto<true>(s, C, T, H, rows, kmajor(w2, H, 0), ng, e3);
+}
+
+void pointwise(hipStream_t s, const float *w, const float *bias, const float *x, int batches, int M, int K, int N,
+               float *out, Act act) {
+    require_ptrs({w, x, out}, "pointwise");
+    EpChannels ep;
+    ep.out = out;
+    ep.bias = bias;
+    ep.batch_stride = (int64_t)M * N;
+    ep.N = N;
+    ep.act = act;
+    gemm_auto<false>(s, M, N, K, batches, kmajor(w, K, 0), MNMajor{x, N, (int64_t)K * N}, ep);
+}
+
+void linear(hipStream_t s, const float *x, int64_t ldx, int64_t x_batch_stride, const float *w, const float *bias,
+            int batches, int M, int K, int N, float *out, int64_t ldo, int64_t out_batch_stride, LinearTail tail,
+            const float *residual, const float *gamma, double *stats) {
+    require_ptrs({x, w, bias, out}, "linear");
+    if (tail == TAIL_RESIDUAL_SCALE) require_ptrs({residual, gamma}, "linear residual");
+    EpLinear ep;
+    ep.out = out;
+    ep.bias = bias;
+    ep.residual = residual;
+    ep.gamma = gamma;
+    ep.stats = stats;
+    ep.ldo = ldo;
+    ep.batch_stride = out_batch_stride;
+    ep.tail = tail;
+    gemm_auto<false>(s, M, N, K, batches, kmajor(x, ldx, x_batch_stride), kmajor(w, K, 0), ep);
+}
+
+void tokens_to_channels(hipStream_t s, const float *tok, int b, int F, int T, int D, const float *w, const float *bias,
+                        int M, float *out) {
+    require_ptrs({tok, w, out}, "tokens_to_channels");
+    DMX_REQUIRE(D % 4 == 0 && aligned16(tok), "tokens_to_channels: token rows must be float4 aligned");
+    EpChannels ep;
+    ep.out = out;
+    ep.bias = bias;
+    ep.batch_stride = (int64_t)M * F * T;
+    ep.N = F * T;
+    ep.act = ACT_NONE;
+    gemm_auto<false>(s, M, F * T, D, b, kmajor(w, D, 0), TokenGather{tok, F, T, D}, ep);
+}
+
+}  // namespace dmx

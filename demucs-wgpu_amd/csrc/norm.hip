@@ -1,0 +1,253 @@
+// norm.hip — LayerNorm, GroupNorm and the elementwise ops of the forward.
+// HBM-bound: each kernel reads and writes its tensor once, float4 where the
+// layout allows, with wave64 shuffle reductions.
+#include "common.h"
+#include "ops.h"
+
+namespace dmx {
+namespace {
+
+// `layer_norm_rows` (crates/demucs-core/src/demucs/ops.rs:596-621): f32 mean,
+// f32 biased variance about it, inv = 1/sqrt(var + 1e-5);
+// out = (x - mean) * inv * w + b (+ add[row % add_rows]). One wave per row.
+__global__ __launch_bounds__(256) void layer_norm_kernel(const float *__restrict__ x, int rows, int dim,
+                                                         const float *__restrict__ w, const float *__restrict__ b,
+                                                         float *__restrict__ out, const float *__restrict__ add,
+                                                         int add_rows) {
+    int row = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+    if (row >= rows) return;
+    const float *xr = x + (int64_t)row * dim;
+    float s = 0.0f;
+    for (int i = lane; i < dim; i += 64) s += xr[i];
+    float mean = wave_sum(s) / (float)dim;
+    float v = 0.0f;
+    for (int i = lane; i < dim; i += 64) {
+        float d = xr[i] - mean;
+        v += d * d;
+    }
+    float var = wave_sum(v) / (float)dim;
+    float inv = 1.0f / sqrtf(var + 1e-5f);
+    float *orow = out + (int64_t)row * dim;
+    const float *ar = add ? add + (int64_t)(row % add_rows) * dim : nullptr;
+    for (int i = lane; i < dim; i += 64) {
+        float y = (xr[i] - mean) * inv * w[i] + b[i];
+        if (ar) y += ar[i];
+        orow[i] = y;
+    }
+}
+
+// (b, c, F*T) channel-major -> LayerNorm'd token rows (b, T*F, c), token = t*F + f,
+// plus pos[token] * pos_weight. A block gathers 16 positions x all channels
+// through LDS so both the read and the write are coalesced.
+constexpr int TOK_POS = 16;
+__global__ __launch_bounds__(256) void channels_to_tokens_ln_kernel(const float *__restrict__ x, int c, int F, int T,
+                                                                    const float *__restrict__ w,
+                                                                    const float *__restrict__ bias,
+                                                                    const float *__restrict__ pos, float pos_weight,
+                                                                    float *__restrict__ out) {
+    extern __shared__ float tile[];  // [c][TOK_POS + 1]
+    const int P = F * T, b = blockIdx.y, p0 = blockIdx.x * TOK_POS;
+    const float *xb = x + (int64_t)b * c * P;
+    for (int e = threadIdx.x; e < c * TOK_POS; e += 256) {
+        int ch = e / TOK_POS, pi = e % TOK_POS, p = p0 + pi;
+        tile[ch * (TOK_POS + 1) + pi] = p < P ? xb[(int64_t)ch * P + p] : 0.0f;
+    }
+    __syncthreads();
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    for (int pi = wave; pi < TOK_POS; pi += 4) {
+        int p = p0 + pi;
+        if (p >= P) break;
+        float s = 0.0f;
+        for (int ch = lane; ch < c; ch += 64) s += tile[ch * (TOK_POS + 1) + pi];
+        float mean = wave_sum(s) / (float)c;
+        float v = 0.0f;
+        for (int ch = lane; ch < c; ch += 64) {
+            float d = tile[ch * (TOK_POS + 1) + pi] - mean;
+            v += d * d;
+        }
+        float var = wave_sum(v) / (float)c;
+        float inv = 1.0f / sqrtf(var + 1e-5f);
+        int f = p / T, t = p - f * T, token = t * F + f;
+        float *orow = out + ((int64_t)b * P + token) * c;
+        const float *prow = pos ? pos + (int64_t)token * c : nullptr;
+        for (int ch = lane; ch < c; ch += 64) {
+            float y = (tile[ch * (TOK_POS + 1) + pi] - mean) * inv * w[ch] + bias[ch];
+            if (prow) y = y + prow[ch] * pos_weight;
+            orow[ch] = y;
+        }
+    }
+}
+
+// MyGroupNorm(1, C) on token planes (crates/demucs-core/src/demucs/host.rs:1137-1196):
+// scale = inv * w[c], shift = bias[c] - mean * scale, x = x * scale + shift.
+__global__ __launch_bounds__(256) void gn_tokens_apply_kernel(float4 *__restrict__ x, int64_t per_batch4, int C4,
+                                                              const double *__restrict__ stats, double count,
+                                                              const float4 *__restrict__ w,
+                                                              const float4 *__restrict__ bias) {
+    const int b = blockIdx.y;
+    float mean, inv;
+    gn_stats(stats + 2 * b, count, mean, inv);
+    float4 *xb = x + b * per_batch4;
+    for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < per_batch4; i += (int64_t)gridDim.x * 256) {
+        int c4 = (int)(i % C4);
+        float4 ww = w[c4], bb = bias[c4], v = xb[i];
+        float sx = inv * ww.x, sy = inv * ww.y, sz = inv * ww.z, sw = inv * ww.w;
+        v.x = v.x * sx + (bb.x - mean * sx);
+        v.y = v.y * sy + (bb.y - mean * sy);
+        v.z = v.z * sz + (bb.z - mean * sz);
+        v.w = v.w * sw + (bb.w - mean * sw);
+        xb[i] = v;
+    }
+}
+
+// f64 moments of each (batch, group) run of `len` floats.
+__global__ __launch_bounds__(256) void moments_kernel(const float *__restrict__ x, int64_t len,
+                                                      double *__restrict__ stats) {
+    const float *p = x + (int64_t)blockIdx.y * len;
+    double s = 0.0, q = 0.0;
+    for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < len; i += (int64_t)gridDim.x * 256) {
+        double v = p[i];
+        s += v;
+        q += v * v;
+    }
+    block_moments_atomic(s, q, stats + 2 * blockIdx.y);
+}
+
+// `group_norm` apply (demucs/ops.rs:583-589).
+__global__ __launch_bounds__(256) void group_norm_apply_kernel(const float *__restrict__ x, int c, int64_t inner,
+                                                               int groups, const float *__restrict__ w,
+                                                               const float *__restrict__ bias,
+                                                               const double *__restrict__ stats,
+                                                               float *__restrict__ out, int64_t total) {
+    int per_group = c / groups;
+    for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < total; i += (int64_t)gridDim.x * 256) {
+        int64_t bc = i / inner;
+        int ch = (int)(bc % c);
+        int64_t b = bc / c;
+        int g = ch / per_group;
+        float mean, inv;
+        gn_stats(stats + 2 * (b * groups + g), (double)per_group * (double)inner, mean, inv);
+        float scale = inv * w[ch];
+        float shift = bias[ch] - mean * scale;
+        out[i] = x[i] * scale + shift;
+    }
+}
+
+// `glu` (demucs/ops.rs:624-658).
+__global__ __launch_bounds__(256) void glu_kernel(const float *__restrict__ x, int c, int64_t inner,
+                                                  float *__restrict__ out, int64_t total) {
+    for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < total; i += (int64_t)gridDim.x * 256) {
+        int64_t row = i / inner, t = i - row * inner;
+        int64_t b = row / c, ch = row % c;
+        const float *value = x + (b * 2 * c + ch) * inner;
+        out[i] = value[t] * sigmoid(value[c * inner + t]);
+    }
+}
+
+__global__ __launch_bounds__(256) void gelu_kernel(const float *__restrict__ x, int64_t n, float *__restrict__ out) {
+    for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256) out[i] = gelu(x[i]);
+}
+
+__global__ __launch_bounds__(256) void zero_f_kernel(float *p, int64_t n) {
+    for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256) p[i] = 0.0f;
+}
+
+__global__ __launch_bounds__(256) void copy_rows_kernel(const float *__restrict__ src, int64_t src_ld, int64_t n_copy,
+                                                        float *__restrict__ dst, int64_t dst_len) {
+    const int64_t r = blockIdx.y;
+    for (int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x; t < dst_len; t += (int64_t)gridDim.x * 256)
+        dst[r * dst_len + t] = t < n_copy ? src[r * src_ld + t] : 0.0f;
+}
+
+__global__ __launch_bounds__(256) void zero_kernel(double *p, int64_t n) {
+    for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256) p[i] = 0.0;
+}
+
+unsigned grid_for(int64_t n, int64_t cap = 8192) {
+    int64_t g = ceil_div(n, 256);
+    return (unsigned)std::max<int64_t>(1, std::min<int64_t>(g, cap));
+}
+
+}  // namespace
+
+void layer_norm_rows(hipStream_t s, const float *x, int rows, int dim, const float *w, const float *b, float *out,
+                     const float *add, int add_rows) {
+    if (rows <= 0) return;
+    require_ptrs({x, w, b, out}, "layer_norm_rows");
+    DMX_REQUIRE(!add || add_rows > 0, "layer_norm_rows: add needs a row count");
+    hipLaunchKernelGGL(layer_norm_kernel, dim3((unsigned)ceil_div(rows, 4)), dim3(256), 0, s, x, rows, dim, w, b, out,
+                       add, add ? add_rows : 1);
+    DMX_LAUNCH_CHECK();
+}
+
+void channels_to_tokens_ln(hipStream_t s, const float *x, int b, int c, int F, int T, const float *w,
+                           const float *bias, const float *pos, float pos_weight, float *out) {
+    require_ptrs({x, w, bias, out}, "channels_to_tokens_ln");
+    size_t shmem = (size_t)c * (TOK_POS + 1) * sizeof(float);
+    DMX_REQUIRE(shmem <= 64 * 1024, "channels_to_tokens_ln: too many channels");
+    dim3 grid((unsigned)ceil_div((int64_t)F * T, TOK_POS), (unsigned)b);
+    hipLaunchKernelGGL(channels_to_tokens_ln_kernel, grid, dim3(256), shmem, s, x, c, F, T, w, bias, pos, pos_weight,
+                       out);
+    DMX_LAUNCH_CHECK();
+}
+
+void group_norm_tokens_apply(hipStream_t s, float *x, int b, int L, int C, const double *stats, const float *w,
+                             const float *bias) {
+    require_ptrs({x, stats, w, bias}, "group_norm_tokens_apply");
+    DMX_REQUIRE(C % 4 == 0, "group_norm_tokens_apply: channels must be a multiple of 4");
+    int64_t per4 = (int64_t)L * C / 4;
+    dim3 grid(grid_for(per4, 2048), (unsigned)b);
+    hipLaunchKernelGGL(gn_tokens_apply_kernel, grid, dim3(256), 0, s, reinterpret_cast<float4 *>(x), per4, C / 4,
+                       stats, (double)L * (double)C, reinterpret_cast<const float4 *>(w),
+                       reinterpret_cast<const float4 *>(bias));
+    DMX_LAUNCH_CHECK();
+}
+
+void group_norm(hipStream_t s, const float *x, int b, int c, int inner, int groups, const float *w, const float *bias,
+                float *out, double *stats) {
+    DMX_REQUIRE(groups > 0 && c % groups == 0, "group_norm: channels not divisible by groups");
+    int64_t len = (int64_t)(c / groups) * inner;
+    zero_doubles(s, stats, 2 * (int64_t)b * groups);
+    hipLaunchKernelGGL(moments_kernel, dim3(grid_for(len, 512), (unsigned)(b * groups)), dim3(256), 0, s, x, len,
+                       stats);
+    DMX_LAUNCH_CHECK();
+    int64_t total = (int64_t)b * c * inner;
+    hipLaunchKernelGGL(group_norm_apply_kernel, dim3(grid_for(total)), dim3(256), 0, s, x, c, (int64_t)inner, groups,
+                       w, bias, stats, out, total);
+    DMX_LAUNCH_CHECK();
+}
+
+void glu(hipStream_t s, const float *x, int b, int c2, int inner, float *out) {
+    DMX_REQUIRE(c2 % 2 == 0, "GLU needs an even channel count");
+    int64_t total = (int64_t)b * (c2 / 2) * inner;
+    hipLaunchKernelGGL(glu_kernel, dim3(grid_for(total)), dim3(256), 0, s, x, c2 / 2, (int64_t)inner, out, total);
+    DMX_LAUNCH_CHECK();
+}
+
+void gelu(hipStream_t s, const float *x, int64_t n, float *out) {
+    hipLaunchKernelGGL(gelu_kernel, dim3(grid_for(n)), dim3(256), 0, s, x, n, out);
+    DMX_LAUNCH_CHECK();
+}
+
+void zero_doubles(hipStream_t s, double *p, int64_t n) {
+    if (n <= 0) return;
+    hipLaunchKernelGGL(zero_kernel, dim3(grid_for(n, 1024)), dim3(256), 0, s, p, n);
+    DMX_LAUNCH_CHECK();
+}
+
+void zero_floats(hipStream_t s, float *p, int64_t n) {
+    if (n <= 0) return;
+    hipLaunchKernelGGL(zero_f_kernel, dim3(grid_for(n, 4096)), dim3(256), 0, s, p, n);
+    DMX_LAUNCH_CHECK();
+}
+
+void copy_rows(hipStream_t s, const float *src, int64_t rows, int64_t src_ld, int64_t n_copy, float *dst,
+               int64_t dst_len) {
+    if (rows <= 0 || dst_len <= 0) return;
+    DMX_REQUIRE(rows <= 65535, "copy_rows: too many rows");
+    hipLaunchKernelGGL(copy_rows_kernel, dim3(grid_for(dst_len, 1024), (unsigned)rows), dim3(256), 0, s, src, src_ld,
+                       n_copy, dst, dst_len);
+    DMX_LAUNCH_CHECK();
+}
+
+}  // namespace dmx

@@ -1,0 +1,126 @@
+// ops.h — host-side launchers of the HIP kernels. Every launcher enqueues on
+// `stream`, validates what the kernel's grid assumes, and never synchronises.
+// Device pointers throughout; layouts follow PyTorch (row-major, (b, c, ...)).
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+namespace dmx {
+
+enum Act { ACT_NONE = 0, ACT_GELU = 1 };
+
+// ---------------- GEMM-based ops (conv.cu / linear.cu) ----------------
+
+// nn.Conv2d over (b, ic, h, w): weight (oc, ic, kh, kw), optional bias; act on output.
+// `skip` (same shape as x, may be null) is added to the input while it is gathered.
+void conv2d(hipStream_t s, const float *x, const float *skip, int b, int ic, int h, int w, const float *weight,
+            const float *bias, int oc, int kh, int kw, int sh, int sw, int ph, int pw, int dh, int dw, float *out,
+            Act act);
+
+// nn.Conv1d over (b, ic, len) after F.pad(x, (0, len_padded - len)) (the time
+// encoder's right pad to a multiple of the stride, host.rs:633-640).
+void conv1d_right_padded(hipStream_t s, const float *x, int b, int ic, int len, int len_padded, const float *weight,
+                         const float *bias, int oc, int k, int stride, int pad, float *out, Act act);
+
+// Conv2d (any kernel, stride 1) whose 2*C output channels feed F.glu(dim=1):
+// out (b, C, oh, ow) = (y[c] + b[c]) * sigmoid(y[C+c] + b[C+c]). When `emb` is
+// given, out[b][c][f][t] += emb_scale * emb[f][c] (the frequency embedding).
+void conv2d_glu(hipStream_t s, const float *x, const float *skip, int b, int ic, int h, int w, const float *weight,
+                const float *bias, int C, int kh, int kw, int ph, int pw, float *out, const float *emb,
+                float emb_scale);
+
+// nn.ConvTranspose along one axis (kernel k, stride st, no padding), cropped:
+// x (b, ic, A, P) -> out (b, oc, a_out, P) with out[a'] = full[a' + crop].
+// weight_packed is (st, oc, ic * taps) from pack_conv_transpose().
+void conv_transpose_axis(hipStream_t s, const float *x, int b, int ic, int A, int P, const float *weight_packed,
+                         const float *bias, int oc, int k, int st, int crop, int a_out, float *out, Act act);
+int conv_transpose_taps(int k, int st);
+// (ic, oc, k) checkpoint layout -> (st, oc, ic*taps) phase-major layout (host arrays).
+void pack_conv_transpose(const float *w, int ic, int oc, int k, int st, float *packed);
+
+// One DConv residual layer (crates/demucs-core/src/demucs/host.rs:985-1059), in
+// place on x, whose rows are (b, f) of a (B, C, F, T) tensor (F = 1 for the
+// waveform branch): conv1d k3 dilation `dil` -> GN(1) -> GELU -> 1x1 -> GN(1)
+// -> GLU -> LayerScale -> +residual. `hbuf` holds (B*F, H, T) floats, `stats`
+// 4*B*F doubles (both scratch).
+void dconv_layer(hipStream_t s, float *x, int B, int C, int F, int T, int dil, const float *w1, const float *b1,
+                 int H, const float *n1w, const float *n1b, const float *w2, const float *b2, const float *n2w,
+                 const float *n2b, const float *gamma, float *hbuf, double *stats);
+
+// out (z, M, N) = W (M, K) . x (z, K, N) + bias[m]  (1x1 conv / channel mixer).
+void pointwise(hipStream_t s, const float *w, const float *bias, const float *x, int batches, int M, int K, int N,
+               float *out, Act act);
+
+// Linear on token rows: out[z][m][n] = x[z][m][:] . W[n][:] + bias[n], with the
+// requested tail. x rows have stride ldx, out rows stride ldo.
+enum LinearTail { TAIL_BIAS = 0, TAIL_BIAS_GELU = 1, TAIL_RESIDUAL_SCALE = 2 };
+void linear(hipStream_t s, const float *x, int64_t ldx, int64_t x_batch_stride, const float *w, const float *bias,
+            int batches, int M, int K, int N, float *out, int64_t ldo, int64_t out_batch_stride, LinearTail tail,
+            const float *residual, const float *gamma, double *stats);
+
+// Channel mixer reading transformer tokens: out (b, M, F*T) with
+// out[z][m][f*T + t] = W[m] . tok[z][t*F + f] + bias[m] (F = 1: token = t).
+void tokens_to_channels(hipStream_t s, const float *tok, int b, int F, int T, int D, const float *w, const float *bias,
+                        int M, float *out);
+
+// ---------------- attention (attention.cu) ----------------
+// Fused softmax(q k^T * scale) v per (batch, head); q/k/v/out are token-major
+// with the head's 64 lanes at column h*64 of rows of stride ld*.
+void attention(hipStream_t s, const float *q, int64_t ldq, const float *k, int64_t ldk, const float *v, int64_t ldv,
+               float *out, int64_t ldo, int batch, int heads, int n_q, int n_k, int d_head, float scale,
+               int64_t q_batch_stride, int64_t kv_batch_stride, int64_t out_batch_stride);
+
+// ---------------- norms / elementwise (norm.cu) ----------------
+void layer_norm_rows(hipStream_t s, const float *x, int rows, int dim, const float *w, const float *b, float *out,
+                     const float *add, int add_rows);
+// (b, c, positions) channel-major -> token rows (b, T*F, c) reordered token = t*F + f,
+// LayerNorm over c, then + pos[token] (pos may be null).
+void channels_to_tokens_ln(hipStream_t s, const float *x, int b, int c, int F, int T, const float *w,
+                           const float *bias, const float *pos, float pos_weight, float *out);
+// GroupNorm(1, C) over whole (L, C) token planes from f64 stats (2 per batch), in place.
+void group_norm_tokens_apply(hipStream_t s, float *x, int b, int L, int C, const double *stats, const float *w,
+                             const float *bias);
+// nn.GroupNorm(groups, c) over (b, c, inner).
+void group_norm(hipStream_t s, const float *x, int b, int c, int inner, int groups, const float *w, const float *bias,
+                float *out, double *stats_scratch);
+void glu(hipStream_t s, const float *x, int b, int c2, int inner, float *out);
+void gelu(hipStream_t s, const float *x, int64_t n, float *out);
+void zero_doubles(hipStream_t s, double *p, int64_t n);
+void zero_floats(hipStream_t s, float *p, int64_t n);
+// dst[r][t] = t < n_copy ? src[r * src_ld + t] : 0 for t < dst_len.
+void copy_rows(hipStream_t s, const float *src, int64_t rows, int64_t src_ld, int64_t n_copy, float *dst,
+               int64_t dst_len);
+
+// ---------------- spectral / framing (spectral.cu) ----------------
+// _spec + pack (CaC) + per-batch normalisation of both branches:
+// mix (b, 2, L) -> xspec (b, 4, nfft/2, le) normalised, xwave (b, 2, L) normalised,
+// norms[4*b] = (mean, std, mean_t, std_t) per batch (f32).
+void spec_and_normalise(hipStream_t s, const float *mix, int b, int L, int nfft, float *spec_raw_frames,
+                        float *xspec, float *xwave, float *norms, double *stats, const float *twiddles);
+// CaC output (b, 4S, nfft/2, le) + time branch (b, 2S, L) -> stems (b, S, 2, L)
+// with both denormalisations and the iSTFT.
+void ispec_and_sum(hipStream_t s, const float *xspec, const float *xtime, int b, int S, int L, int nfft, int le,
+                   const float *norms, float *frames_scratch, float *stems, const float *twiddles);
+// Raw STFT pieces for op-level checks.
+void stft_cac_raw(hipStream_t s, const float *mix, int b, int L, int nfft, float *frames_out, float *xspec_out,
+                  const float *twiddles);
+void make_twiddles(int nfft, float *host_out);  // nfft/2 complex (cos, -sin) pairs
+
+// ---------------- chunking / overlap-add (pipeline.cu) ----------------
+void mix_moments(hipStream_t s, const float *mix, int64_t samples, double *stats);
+void build_chunks(hipStream_t s, const float *mix, int64_t mix_len, const double *stats, int group, const int64_t *starts,
+                  const int64_t *lengths, int64_t seg, int64_t view_len, int64_t shift_offset, int64_t max_shift,
+                  float *out);
+void ola_accumulate(hipStream_t s, const float *chunk_out, int group, const int64_t *starts, const int64_t *lengths,
+                    int64_t seg, int rows, int64_t view_len, const float *weight, float *acc, float *sum_w);
+void ola_finish(hipStream_t s, const float *acc, const float *sum_w, int rows, int64_t view_len, int64_t trim,
+                int64_t samples, const double *stats, float scale, int accumulate, float *stems,
+                const uint8_t *row_mask);
+void bag_accumulate(hipStream_t s, const float *net_out, int64_t group_batch, int sources, int64_t per_source,
+                    const float *weights, float *combined, int first);
+void bag_divide(hipStream_t s, float *combined, int64_t group_batch, int sources, int64_t per_source,
+                const float *totals);
+
+}  // namespace dmx

@@ -1,0 +1,1154 @@
+// runner.hip — the HTDemucs segment forward on one MI355X, and the C-ABI of
+// include/dmx.h around it.
+//
+// The forward walks the graph of `Htdemucs::forward`
+// (crates/demucs-core/src/demucs/host.rs:202-520) with one fused launch per
+// op group; every intermediate lives in HBM in the reference's own layout
+// ((b, c, f, t) for the branches, (b, tokens, c) inside the transformer), so a
+// traced activation needs no conversion. Intermediates come from the
+// stream-ordered pool (hipMallocAsync / hipFreeAsync on the runner's stream),
+// which recycles them without host synchronisation.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cmath>
+#include <cstring>
+#include <map>
+#include <memory>
+#include <mutex>
+#include <string>
+#include <vector>
+
+#include "../../include/dmx.h"
+#include "common.h"
+#include "ops.h"
+
+namespace dmx {
+namespace {
+
+
+// A device buffer from the runner stream's pool; freed (stream-ordered) on scope exit.
+struct DBuf {
+    hipStream_t s = nullptr;
+    void *p = nullptr;
+    size_t bytes = 0;
+    DBuf() = default;
+    DBuf(hipStream_t stream, size_t n_bytes) : s(stream), bytes(n_bytes) {
+        if (bytes) DMX_HIP(hipMallocAsync(&p, bytes, s));
+    }
+    DBuf(const DBuf &) = delete;
+    DBuf &operator=(const DBuf &) = delete;
+    DBuf(DBuf &&o) noexcept : s(o.s), p(o.p), bytes(o.bytes) { o.p = nullptr; }
+    DBuf &operator=(DBuf &&o) noexcept {
+        if (this != &o) {
+            release();
+            s = o.s;
+            p = o.p;
+            bytes = o.bytes;
+            o.p = nullptr;
+        }
+        return *this;
+    }
+    ~DBuf() { release(); }
+    void release() {
+        if (p) (void)hipFreeAsync(p, s);
+        p = nullptr;
+    }
+    float *f() const { return static_cast<float *>(p); }
+    double *d() const { return static_cast<double *>(p); }
+};
+
+DBuf fbuf(hipStream_t s, int64_t n) { return DBuf(s, (size_t)std::max<int64_t>(n, 1) * sizeof(float)); }
+DBuf dbuf(hipStream_t s, int64_t n) { return DBuf(s, (size_t)std::max<int64_t>(n, 1) * sizeof(double)); }
+
+struct Trace {
+    dmx_trace_wants_fn wants = nullptr;
+    dmx_trace_record_fn record = nullptr;
+    void *user = nullptr;
+};
+
+struct DConvW {
+    const float *w1, *b1, *n1w, *n1b, *w2, *b2, *n2w, *n2b, *gamma;
+    int hidden;
+};
+
+struct LayerW {
+    const float *conv_w = nullptr, *conv_b = nullptr, *rw = nullptr, *rb = nullptr;
+    int cin = 0, cout = 0;
+    DConvW dconv[2];
+};
+
+struct TLayerW {
+    bool cross;
+    const float *in_w, *in_b, *out_w, *out_b, *w1, *b1, *w2, *b2;
+    const float *n1w, *n1b, *n2w, *n2b, *n3w, *n3b, *now_, *nob, *g1, *g2;
+};
+
+}  // namespace
+}  // namespace dmx
+
+struct dmx_pending {
+    float *host_in = nullptr;   // pinned staging of the caller's mix
+    float *host_out = nullptr;  // pinned
+    size_t count = 0;
+    hipEvent_t done = nullptr;
+};
+
+struct dmx_runner {
+    dmx_config cfg{};
+    int device = 0;
+    int precision = 0;
+    hipStream_t stream = nullptr;
+    std::string tag;
+    int64_t training_length = 0;
+    int hop = 0, pre_channels = 0, tch = 0, hidden = 0, freq_emb_rows = 0;
+
+    void *weight_mem = nullptr;
+    std::map<std::string, float *> w;
+    std::vector<dmx::LayerW> enc, tenc, dec, tdec;  // decoders in execution order
+    float *freq_emb = nullptr;                      // (rows, channels) x emb_scale
+    std::vector<dmx::TLayerW> layers, layers_t;
+    float *twiddles = nullptr;                      // nfft/2 complex + nfft window
+    std::map<std::pair<int64_t, int64_t>, float *> pos2d;  // (freqs, frames) -> (T*F, D)
+    std::map<int64_t, float *> pos1d;                       // length -> (L, D)
+    std::map<int64_t, float *> ola_weights;                 // segment -> (seg)
+    std::vector<void *> owned;                              // device blocks freed at destroy
+    float *eye = nullptr;                                   // (D, D) identity + D zeros
+    dmx::Trace trace;
+};
+
+namespace dmx {
+namespace {
+
+float *dev(dmx_runner &r, const std::string &name) {
+    auto it = r.w.find(name);
+    if (it == r.w.end()) throw_error(DMX_ERR_MISSING_WEIGHT, "weight `" + name + "` not found in checkpoint");
+    return it->second;
+}
+
+float *upload(dmx_runner &r, const std::vector<float> &host) {
+    void *p = nullptr;
+    DMX_HIP(hipMalloc(&p, std::max<size_t>(host.size(), 1) * sizeof(float)));
+    r.owned.push_back(p);
+    if (!host.empty()) DMX_HIP(hipMemcpy(p, host.data(), host.size() * sizeof(float), hipMemcpyHostToDevice));
+    return static_cast<float *>(p);
+}
+
+bool wants(const dmx_runner &r, const std::string &name) {
+    return r.trace.record && (!r.trace.wants || r.trace.wants(name.c_str(), r.trace.user));
+}
+
+void record(dmx_runner &r, const std::string &name, const float *d, std::initializer_list<int64_t> shape) {
+    if (!wants(r, name)) return;
+    std::vector<int64_t> s(shape);
+    int64_t n = 1;
+    for (int64_t v : s) n *= v;
+    std::vector<float> host((size_t)n);
+    DMX_HIP(hipStreamSynchronize(r.stream));
+    DMX_HIP(hipMemcpy(host.data(), d, (size_t)n * sizeof(float), hipMemcpyDeviceToHost));
+    r.trace.record(name.c_str(), s.data(), (int32_t)s.size(), host.data(), r.trace.user);
+}
+
+// `HtdemucsConfig::validate` (crates/demucs-core/src/demucs/config.rs:239-273).
+void validate(const dmx_config &c) {
+    auto unsupported = [](const char *what) {
+        throw_error(DMX_ERR_UNSUPPORTED, std::string("htdemucs config: ") + what + " is not supported by this port");
+    };
+    if (!c.cac) unsupported("cac = false (magnitude masking)");
+    if (c.nfft != 4096) unsupported("nfft != 4096");
+    if (c.kernel_size != 8 || c.stride != 4) unsupported("kernel_size/stride other than 8/4");
+    if (c.audio_channels != 2) unsupported("audio_channels != 2");
+    if (c.sources != 4) unsupported("a source count other than 4");
+    int freqs = c.nfft / 2;
+    for (int i = 0; i < c.depth; ++i) {
+        if (freqs > 1 && freqs <= c.kernel_size) unsupported("a `last_freq` layer");
+        if (freqs > 1) freqs /= c.stride;
+    }
+    if (c.context != 1) unsupported("context != 1");
+    if (c.bottom_channels <= 0) unsupported("bottom_channels = 0");
+    if (c.t_heads <= 0 || c.bottom_channels % c.t_heads || c.bottom_channels / c.t_heads != 64)
+        unsupported("a head width other than 64");
+    if (c.segment <= 0.0) throw_error(DMX_ERR_CONFIG, "segment must be positive");
+}
+
+// Positional embeddings (host.rs:1078-1122), computed once per shape on the host.
+float *pos2d_for(dmx_runner &r, int64_t freqs, int64_t frames) {
+    auto key = std::make_pair(freqs, frames);
+    auto it = r.pos2d.find(key);
+    if (it != r.pos2d.end()) return it->second;
+    const int64_t dim = r.tch, half = dim / 2, pairs = half / 2;
+    const float max_period = (float)r.cfg.t_max_period;
+    const float log_period = std::log(max_period) / (float)half;
+    std::vector<float> div(pairs), out(frames * freqs * dim);
+    for (int64_t j = 0; j < pairs; ++j) div[j] = std::exp(-(float)(2 * j) * log_period);
+    for (int64_t t = 0; t < frames; ++t)
+        for (int64_t f = 0; f < freqs; ++f) {
+            float *tok = out.data() + (t * freqs + f) * dim;
+            for (int64_t j = 0; j < pairs; ++j) {
+                float a = (float)t * div[j], b = (float)f * div[j];
+                tok[2 * j] = std::sin(a);
+                tok[2 * j + 1] = std::cos(a);
+                tok[half + 2 * j] = std::sin(b);
+                tok[half + 2 * j + 1] = std::cos(b);
+            }
+        }
+    return r.pos2d[key] = upload(r, out);
+}
+
+float *pos1d_for(dmx_runner &r, int64_t length) {
+    auto it = r.pos1d.find(length);
+    if (it != r.pos1d.end()) return it->second;
+    const int64_t dim = r.tch, half = dim / 2;
+    const float max_period = (float)r.cfg.t_max_period;
+    std::vector<float> out(length * dim);
+    for (int64_t t = 0; t < length; ++t)
+        for (int64_t i = 0; i < half; ++i) {
+            float exponent = (float)i / ((float)half - 1.0f);
+            float phase = (float)t / std::pow(max_period, exponent);
+            out[t * dim + i] = std::cos(phase);
+            out[t * dim + half + i] = std::sin(phase);
+        }
+    return r.pos1d[length] = upload(r, out);
+}
+
+// `transition_weight` (crates/demucs-core/src/demucs/pipeline.rs:117-131), power 1.
+std::vector<float> transition_weight(int64_t n, double power) {
+    std::vector<float> w;
+    w.reserve(n);
+    int64_t half = n / 2;
+    for (int64_t i = 1; i <= half; ++i) w.push_back((float)i);
+    for (int64_t i = n - half; i >= 1; --i) w.push_back((float)i);
+    float mx = 1.0f;
+    for (float v : w) mx = std::max(mx, v);
+    for (float &v : w) v = std::pow(v / mx, (float)power);
+    return w;
+}
+
+// ----- the forward -----
+
+void run_dconv(dmx_runner &r, hipStream_t s, float *x, int B, int C, int F, int T, const LayerW &L) {
+    const int rows = B * F;
+    for (int d = 0; d < 2; ++d) {
+        const DConvW &D = L.dconv[d];
+        DBuf h = fbuf(s, (int64_t)rows * D.hidden * T);
+        DBuf st = dbuf(s, 4 * (int64_t)rows);
+        dconv_layer(s, x, B, C, F, T, 1 << d, D.w1, D.b1, D.hidden, D.n1w, D.n1b, D.w2, D.b2, D.n2w, D.n2b, D.gamma,
+                    h.f(), st.d());
+    }
+    (void)r;
+}
+
+// One `classic_layer_forward` / `cross_layer_forward` (host.rs:1315-1429) on
+// token planes; returns the new plane (GroupNorm applied).
+DBuf transformer_layer(dmx_runner &r, hipStream_t s, const TLayerW &L, const float *xq, int64_t Lq, const float *xkv,
+                       int64_t Lk, int B, const std::string &name) {
+    const int D = r.tch, H = r.hidden, heads = r.cfg.t_heads;
+    const float scale = 1.0f / std::sqrt((float)(D / heads));
+    DBuf nq = fbuf(s, B * Lq * D);
+    layer_norm_rows(s, xq, (int)(B * Lq), D, L.n1w, L.n1b, nq.f(), nullptr, 0);
+    DBuf att = fbuf(s, B * Lq * D);
+    if (L.cross) {
+        DBuf nk = fbuf(s, B * Lk * D);
+        layer_norm_rows(s, xkv, (int)(B * Lk), D, L.n2w, L.n2b, nk.f(), nullptr, 0);
+        DBuf q = fbuf(s, B * Lq * D), kv = fbuf(s, B * Lk * 2 * D);
+        linear(s, nq.f(), D, Lq * D, L.in_w, L.in_b, B, (int)Lq, D, D, q.f(), D, Lq * D, TAIL_BIAS, nullptr, nullptr,
+               nullptr);
+        linear(s, nk.f(), D, Lk * D, L.in_w + (int64_t)D * D, L.in_b + D, B, (int)Lk, D, 2 * D, kv.f(), 2 * D,
+               Lk * 2 * D, TAIL_BIAS, nullptr, nullptr, nullptr);
+        attention(s, q.f(), D, kv.f(), 2 * D, kv.f() + D, 2 * D, att.f(), D, B, heads, (int)Lq, (int)Lk, D / heads,
+                  scale, Lq * D, Lk * 2 * D, Lq * D);
+    } else {
+        DBuf qkv = fbuf(s, B * Lq * 3 * D);
+        linear(s, nq.f(), D, Lq * D, L.in_w, L.in_b, B, (int)Lq, D, 3 * D, qkv.f(), 3 * D, Lq * 3 * D, TAIL_BIAS,
+               nullptr, nullptr, nullptr);
+        attention(s, qkv.f(), 3 * D, qkv.f() + D, 3 * D, qkv.f() + 2 * D, 3 * D, att.f(), D, B, heads, (int)Lq,
+                  (int)Lq, D / heads, scale, Lq * 3 * D, Lq * 3 * D, Lq * D);
+    }
+    DBuf x1 = fbuf(s, B * Lq * D);
+    linear(s, att.f(), D, Lq * D, L.out_w, L.out_b, B, (int)Lq, D, D, x1.f(), D, Lq * D, TAIL_RESIDUAL_SCALE, xq, L.g1,
+           nullptr);
+    DBuf n2 = fbuf(s, B * Lq * D);
+    if (L.cross)
+        layer_norm_rows(s, x1.f(), (int)(B * Lq), D, L.n3w, L.n3b, n2.f(), nullptr, 0);
+    else
+        layer_norm_rows(s, x1.f(), (int)(B * Lq), D, L.n2w, L.n2b, n2.f(), nullptr, 0);
+    DBuf hid = fbuf(s, B * Lq * H);
+    linear(s, n2.f(), D, Lq * D, L.w1, L.b1, B, (int)Lq, D, H, hid.f(), H, Lq * H, TAIL_BIAS_GELU, nullptr, nullptr,
+           nullptr);
+    DBuf out = fbuf(s, B * Lq * D);
+    DBuf stats = dbuf(s, 2 * B);
+    zero_doubles(s, stats.d(), 2 * B);
+    linear(s, hid.f(), H, Lq * H, L.w2, L.b2, B, (int)Lq, H, D, out.f(), D, Lq * D, TAIL_RESIDUAL_SCALE, x1.f(), L.g2,
+           stats.d());
+    group_norm_tokens_apply(s, out.f(), B, (int)Lq, D, stats.d(), L.now_, L.nob);
+    record(r, name, out.f(), {B, Lq, D});
+    return out;
+}
+
+// `transformer_forward` (host.rs:830-946): x (B, D, F, T), xt (B, D, Lt) channel-major.
+void transformer(dmx_runner &r, hipStream_t s, const float *x, const float *xt, int B, int F, int T, int Lt,
+                 float *x_out, float *xt_out) {
+    const int D = r.tch;
+    const int64_t Lf = (int64_t)F * T;
+    const float wpe = (float)r.cfg.t_weight_pos_embed;
+    DBuf spec = fbuf(s, B * Lf * D), time = fbuf(s, (int64_t)B * Lt * D);
+    channels_to_tokens_ln(s, x, B, D, F, T, dev(r, "crosstransformer.norm_in.weight"),
+                          dev(r, "crosstransformer.norm_in.bias"), pos2d_for(r, F, T), wpe, spec.f());
+    channels_to_tokens_ln(s, xt, B, D, 1, Lt, dev(r, "crosstransformer.norm_in_t.weight"),
+                          dev(r, "crosstransformer.norm_in_t.bias"), pos1d_for(r, Lt), wpe, time.f());
+    record(r, "crosstransformer.in#0", spec.f(), {B, Lf, D});
+    record(r, "crosstransformer.in#1", time.f(), {B, Lt, D});
+    for (int i = 0; i < r.cfg.t_layers; ++i) {
+        std::string n = "crosstransformer.layers." + std::to_string(i);
+        std::string nt = "crosstransformer.layers_t." + std::to_string(i);
+        if (r.layers[i].cross) {
+            DBuf ns = transformer_layer(r, s, r.layers[i], spec.f(), Lf, time.f(), Lt, B, n);
+            DBuf nt_ = transformer_layer(r, s, r.layers_t[i], time.f(), Lt, spec.f(), Lf, B, nt);
+            spec = std::move(ns);
+            time = std::move(nt_);
+        } else {
+            spec = transformer_layer(r, s, r.layers[i], spec.f(), Lf, nullptr, 0, B, n);
+            time = transformer_layer(r, s, r.layers_t[i], time.f(), Lt, nullptr, 0, B, nt);
+        }
+    }
+    // The channel downsamplers read the token planes directly.
+    tokens_to_channels(s, spec.f(), B, F, T, D, dev(r, "channel_downsampler.weight"), dev(r, "channel_downsampler.bias"),
+                       r.pre_channels, x_out);
+    tokens_to_channels(s, time.f(), B, 1, Lt, D, dev(r, "channel_downsampler_t.weight"),
+                       dev(r, "channel_downsampler_t.bias"), r.pre_channels, xt_out);
+}
+
+// Stack-only entry point: same prologue/layers, outputs rearranged back to
+// (B, D, F, T) / (B, D, Lt) without the channel mixers.
+void transformer_only(dmx_runner &r, hipStream_t s, const float *x, const float *xt, int B, int F, int T, int Lt,
+                      float *x_out, float *xt_out) {
+    const int D = r.tch;
+    const int64_t Lf = (int64_t)F * T;
+    const float wpe = (float)r.cfg.t_weight_pos_embed;
+    DBuf spec = fbuf(s, B * Lf * D), time = fbuf(s, (int64_t)B * Lt * D);
+    channels_to_tokens_ln(s, x, B, D, F, T, dev(r, "crosstransformer.norm_in.weight"),
+                          dev(r, "crosstransformer.norm_in.bias"), pos2d_for(r, F, T), wpe, spec.f());
+    channels_to_tokens_ln(s, xt, B, D, 1, Lt, dev(r, "crosstransformer.norm_in_t.weight"),
+                          dev(r, "crosstransformer.norm_in_t.bias"), pos1d_for(r, Lt), wpe, time.f());
+    for (int i = 0; i < r.cfg.t_layers; ++i) {
+        std::string n = "crosstransformer.layers." + std::to_string(i);
+        std::string nt = "crosstransformer.layers_t." + std::to_string(i);
+        if (r.layers[i].cross) {
+            DBuf ns = transformer_layer(r, s, r.layers[i], spec.f(), Lf, time.f(), Lt, B, n);
+            DBuf nt_ = transformer_layer(r, s, r.layers_t[i], time.f(), Lt, spec.f(), Lf, B, nt);
+            spec = std::move(ns);
+            time = std::move(nt_);
+        } else {
+            spec = transformer_layer(r, s, r.layers[i], spec.f(), Lf, nullptr, 0, B, n);
+            time = transformer_layer(r, s, r.layers_t[i], time.f(), Lt, nullptr, 0, B, nt);
+        }
+    }
+    // The rearrange back to (B, D, F, T) reuses the token-gather GEMM with an
+    // identity matrix (exact: every output is one product by 1.0 plus zeros).
+    if (!r.eye) {
+        std::vector<float> eye((size_t)D * D + D, 0.0f);
+        for (int i = 0; i < D; ++i) eye[(size_t)i * D + i] = 1.0f;
+        r.eye = upload(r, eye);
+    }
+    tokens_to_channels(s, spec.f(), B, F, T, D, r.eye, r.eye + (size_t)D * D, D, x_out);
+    tokens_to_channels(s, time.f(), B, 1, Lt, D, r.eye, r.eye + (size_t)D * D, D, xt_out);
+}
+
+// `Htdemucs::forward` on device: mix (B, 2, L) with L == training_length -> stems (B, S, 2, L).
+void forward_full(dmx_runner &r, hipStream_t s, const float *mix, int B, float *stems) {
+    const dmx_config &c = r.cfg;
+    const int L = (int)r.training_length, nfft = c.nfft, hop = r.hop, le = (int)ceil_div(L, hop), bins = nfft / 2;
+    DBuf frames = fbuf(s, (int64_t)B * 2 * le * bins * 2);
+    DBuf xspec = fbuf(s, (int64_t)B * 4 * bins * le);
+    DBuf xwave = fbuf(s, (int64_t)B * 2 * L);
+    DBuf norms = fbuf(s, 4 * (int64_t)B);
+    DBuf nstats = dbuf(s, 4 * (int64_t)B);
+    spec_and_normalise(s, mix, B, L, nfft, frames.f(), xspec.f(), xwave.f(), norms.f(), nstats.d(), r.twiddles);
+    frames.release();
+    record(r, "x_normalized", xspec.f(), {B, 4, bins, le});
+    record(r, "xt_normalized", xwave.f(), {B, 2, L});
+
+    const int depth = c.depth;
+    std::vector<DBuf> saved, saved_t;
+    std::vector<int> lengths_t, fdims;
+    // Each encoder layer reads the previous layer's output, which is also the
+    // skip connection kept in saved / saved_t.
+    const float *x_in = xspec.f(), *xt_in = xwave.f();
+    int cin = 4, F = bins, tcin = 2, tlen = L;
+    for (int i = 0; i < depth; ++i) {
+        // Waveform encoder (host.rs:625-678).
+        const LayerW &TL = r.tenc[i];
+        lengths_t.push_back(tlen);
+        int padded = tlen % 4 ? tlen + (4 - tlen % 4) : tlen;
+        int tout = (padded + 4 - 8) / 4 + 1;
+        DBuf y = fbuf(s, (int64_t)B * TL.cout * tout);
+        conv1d_right_padded(s, xt_in, B, tcin, tlen, padded, TL.conv_w, TL.conv_b, TL.cout, 8, 4, 2, y.f(), ACT_GELU);
+        run_dconv(r, s, y.f(), B, TL.cout, 1, tout, TL);
+        DBuf xt_next = fbuf(s, (int64_t)B * TL.cout * tout);
+        conv2d_glu(s, y.f(), nullptr, B, TL.cout, 1, tout, TL.rw, TL.rb, TL.cout, 1, 1, 0, 0, xt_next.f(), nullptr, 0.f);
+        tcin = TL.cout;
+        tlen = tout;
+        record(r, "tencoder." + std::to_string(i), xt_next.f(), {B, tcin, tlen});
+        xt_in = xt_next.f();
+        saved_t.push_back(std::move(xt_next));
+        // Frequency encoder (host.rs:577-622).
+        const LayerW &FL = r.enc[i];
+        int fout = (F + 4 - 8) / 4 + 1;
+        DBuf yf = fbuf(s, (int64_t)B * FL.cout * fout * le);
+        conv2d(s, x_in, nullptr, B, cin, F, le, FL.conv_w, FL.conv_b, FL.cout, 8, 1, 4, 1, 2, 0, 1, 1, yf.f(), ACT_GELU);
+        run_dconv(r, s, yf.f(), B, FL.cout, fout, le, FL);
+        DBuf x_next = fbuf(s, (int64_t)B * FL.cout * fout * le);
+        const bool emb = i == 0 && c.freq_emb > 0.0;
+        if (emb) DMX_REQUIRE(fout == r.freq_emb_rows && FL.cout == c.channels, "frequency embedding shape mismatch");
+        conv2d_glu(s, yf.f(), nullptr, B, FL.cout, fout, le, FL.rw, FL.rb, FL.cout, 1, 1, 0, 0, x_next.f(),
+                   emb ? r.freq_emb : nullptr, (float)c.freq_emb);
+        cin = FL.cout;
+        F = fout;
+        if (wants(r, "encoder." + std::to_string(i)) && !emb)
+            record(r, "encoder." + std::to_string(i), x_next.f(), {B, cin, F, le});
+        if (emb) record(r, "encoder.0.post_emb", x_next.f(), {B, cin, F, le});
+        x_in = x_next.f();
+        saved.push_back(std::move(x_next));
+    }
+    xspec.release();
+    xwave.release();
+    const float *xin = saved.back().f();
+    const float *xtin = saved_t.back().f();
+    // Channel upsamplers (host.rs:320-339) then the transformer.
+    const int D = r.tch, P = r.pre_channels;
+    DBuf up = fbuf(s, (int64_t)B * D * F * le), upt = fbuf(s, (int64_t)B * D * tlen);
+    pointwise(s, dev(r, "channel_upsampler.weight"), dev(r, "channel_upsampler.bias"), xin, B, D, P, F * le, up.f(),
+              ACT_NONE);
+    pointwise(s, dev(r, "channel_upsampler_t.weight"), dev(r, "channel_upsampler_t.bias"), xtin, B, D, P, tlen,
+              upt.f(), ACT_NONE);
+    record(r, "channel_upsampler", up.f(), {B, D, (int64_t)F * le});
+    record(r, "channel_upsampler_t", upt.f(), {B, D, tlen});
+    DBuf xd = fbuf(s, (int64_t)B * P * F * le), xtd = fbuf(s, (int64_t)B * P * tlen);
+    transformer(r, s, up.f(), upt.f(), B, F, le, tlen, xd.f(), xtd.f());
+    up.release();
+    upt.release();
+    record(r, "channel_downsampler", xd.f(), {B, P, (int64_t)F * le});
+    record(r, "channel_downsampler_t", xtd.f(), {B, P, tlen});
+
+    DBuf x = std::move(xd), xt = std::move(xtd);
+    cin = P;
+    tcin = P;
+    for (int i = 0; i < depth; ++i) {
+        const bool last = i == depth - 1;
+        // Frequency decoder (host.rs:682-759).
+        const LayerW &FL = r.dec[i];
+        DBuf skip = std::move(saved.back());
+        saved.pop_back();
+        DBuf g = fbuf(s, (int64_t)B * cin * F * le);
+        conv2d_glu(s, x.f(), skip.f(), B, cin, F, le, FL.rw, FL.rb, cin, 3, 3, 1, 1, g.f(), nullptr, 0.f);
+        skip.release();
+        run_dconv(r, s, g.f(), B, cin, F, le, FL);
+        record(r, "decoder." + std::to_string(i) + "#1", g.f(), {B, cin, F, le});
+        int fout = 4 * F;
+        DBuf z = fbuf(s, (int64_t)B * FL.cout * fout * le);
+        conv_transpose_axis(s, g.f(), B, cin, F, le, FL.conv_w, FL.conv_b, FL.cout, 8, 4, 2, fout, z.f(),
+                            last ? ACT_NONE : ACT_GELU);
+        record(r, "decoder." + std::to_string(i) + "#0", z.f(), {B, FL.cout, fout, le});
+        x = std::move(z);
+        cin = FL.cout;
+        F = fout;
+        // Waveform decoder (host.rs:763-827).
+        const LayerW &TL = r.tdec[i];
+        DBuf skip_t = std::move(saved_t.back());
+        saved_t.pop_back();
+        int length_t = lengths_t.back();
+        lengths_t.pop_back();
+        DBuf gt = fbuf(s, (int64_t)B * tcin * tlen);
+        conv2d_glu(s, xt.f(), skip_t.f(), B, tcin, 1, tlen, TL.rw, TL.rb, tcin, 1, 3, 0, 1, gt.f(), nullptr, 0.f);
+        skip_t.release();
+        run_dconv(r, s, gt.f(), B, tcin, 1, tlen, TL);
+        record(r, "tdecoder." + std::to_string(i) + "#1", gt.f(), {B, tcin, tlen});
+        DBuf zt = fbuf(s, (int64_t)B * TL.cout * length_t);
+        conv_transpose_axis(s, gt.f(), B, tcin, tlen, 1, TL.conv_w, TL.conv_b, TL.cout, 8, 4, 2, length_t, zt.f(),
+                            last ? ACT_NONE : ACT_GELU);
+        record(r, "tdecoder." + std::to_string(i) + "#0", zt.f(), {B, TL.cout, length_t});
+        xt = std::move(zt);
+        tcin = TL.cout;
+        tlen = length_t;
+    }
+    DMX_REQUIRE(cin == c.sources * 4 && tcin == c.sources * 2 && tlen == L, "decoder output shapes are wrong");
+    const int S = c.sources, rows = B * S * 2;
+    DBuf scratch = fbuf(s, (int64_t)rows * le * nfft + (int64_t)rows * le * bins * 2);
+    ispec_and_sum(s, x.f(), xt.f(), B, S, L, nfft, le, norms.f(), scratch.f(), stems, r.twiddles);
+    record(r, "model_out", stems, {B, S, 2, L});
+}
+
+// Forward with any length <= training_length: zero pad in, crop out.
+void forward_device(dmx_runner &r, hipStream_t s, const float *mix, int64_t B, int64_t channels, int64_t length,
+                    float *stems) {
+    if (channels != r.cfg.audio_channels)
+        throw_error(DMX_ERR_SHAPE, "expected " + std::to_string(r.cfg.audio_channels) + " audio channels, got " +
+                                       std::to_string(channels));
+    const int64_t L = r.training_length;
+    if (length > L)
+        throw_error(DMX_ERR_SHAPE, "input is " + std::to_string(length) + " samples but the model segment is " +
+                                       std::to_string(L) + "; chunk the audio before calling forward");
+    if (B <= 0 || length <= 0) throw_error(DMX_ERR_SHAPE, "empty input");
+    const int S = r.cfg.sources;
+    if (length == L) {
+        forward_full(r, s, mix, (int)B, stems);
+        return;
+    }
+    DBuf padded = fbuf(s, B * channels * L), full = fbuf(s, B * S * 2 * L);
+    copy_rows(s, mix, B * channels, length, length, padded.f(), L);
+    forward_full(r, s, padded.f(), (int)B, full.f());
+    copy_rows(s, full.f(), B * S * 2, L, length, stems, length);
+}
+
+// ----- weights -----
+
+void load_weights(dmx_runner &r, const dmx_tensor *weights, size_t n) {
+    const dmx_config &c = r.cfg;
+    // Expected shapes (crates/demucs-core/src/demucs/weights.rs:224-578, config.rs:325-444).
+    std::map<std::string, std::vector<int64_t>> expect;
+    std::map<std::string, const dmx_tensor *> given;
+    for (size_t i = 0; i < n; ++i) {
+        if (!weights[i].name || !weights[i].data) throw_error(DMX_ERR_ARGUMENT, "weight entry without name or data");
+        given[weights[i].name] = &weights[i];
+    }
+    const int depth = c.depth, hidden_div = 8;
+    int chin = c.audio_channels, chin_z = chin * 2, chout = c.channels, chout_z = c.channels, freqs = c.nfft / 2;
+    struct Spec {
+        int chin, chout;
+    };
+    std::vector<Spec> dspec, tdspec;
+    auto dconv_shapes = [&](const std::string &p, int ch) {
+        int hid = ch / hidden_div;
+        for (int d = 0; d < 2; ++d) {
+            std::string at = p + ".layers." + std::to_string(d);
+            expect[at + ".0.weight"] = {hid, ch, 3};
+            expect[at + ".0.bias"] = {hid};
+            expect[at + ".1.weight"] = {hid};
+            expect[at + ".1.bias"] = {hid};
+            expect[at + ".3.weight"] = {2 * ch, hid, 1};
+            expect[at + ".3.bias"] = {2 * ch};
+            expect[at + ".4.weight"] = {2 * ch};
+            expect[at + ".4.bias"] = {2 * ch};
+            expect[at + ".6.scale"] = {ch};
+        }
+    };
+    for (int i = 0; i < depth; ++i) {
+        std::string e = "encoder." + std::to_string(i), te = "tencoder." + std::to_string(i);
+        expect[e + ".conv.weight"] = {chout_z, chin_z, 8, 1};
+        expect[e + ".conv.bias"] = {chout_z};
+        expect[e + ".rewrite.weight"] = {2 * chout_z, chout_z, 1, 1};
+        expect[e + ".rewrite.bias"] = {2 * chout_z};
+        dconv_shapes(e + ".dconv", chout_z);
+        expect[te + ".conv.weight"] = {chout, chin, 8};
+        expect[te + ".conv.bias"] = {chout};
+        expect[te + ".rewrite.weight"] = {2 * chout, chout, 1};
+        expect[te + ".rewrite.bias"] = {2 * chout};
+        dconv_shapes(te + ".dconv", chout);
+        if (i == 0) {
+            chin = c.audio_channels * c.sources;
+            chin_z = chin * 2;
+        }
+        dspec.push_back({chout_z, chin_z});
+        tdspec.push_back({chout, chin});
+        if (i == 0) r.freq_emb_rows = freqs / c.stride;
+        chin = chout;
+        chin_z = chout_z;
+        chout *= c.growth;
+        chout_z *= c.growth;
+        freqs /= c.stride;
+    }
+    for (int i = 0; i < depth; ++i) {
+        std::string d = "decoder." + std::to_string(i), td = "tdecoder." + std::to_string(i);
+        expect[d + ".conv_tr.weight"] = {dspec[i].chin, dspec[i].chout, 8, 1};
+        expect[d + ".conv_tr.bias"] = {dspec[i].chout};
+        expect[d + ".rewrite.weight"] = {2 * dspec[i].chin, dspec[i].chin, 3, 3};
+        expect[d + ".rewrite.bias"] = {2 * dspec[i].chin};
+        dconv_shapes(d + ".dconv", dspec[i].chin);
+        expect[td + ".conv_tr.weight"] = {tdspec[i].chin, tdspec[i].chout, 8};
+        expect[td + ".conv_tr.bias"] = {tdspec[i].chout};
+        expect[td + ".rewrite.weight"] = {2 * tdspec[i].chin, tdspec[i].chin, 3};
+        expect[td + ".rewrite.bias"] = {2 * tdspec[i].chin};
+        dconv_shapes(td + ".dconv", tdspec[i].chin);
+    }
+    r.pre_channels = chin_z;
+    r.tch = c.bottom_channels;
+    r.hidden = (int)((double)r.tch * c.t_hidden_scale);
+    const int D = r.tch, P = r.pre_channels, H = r.hidden;
+    expect["freq_emb.embedding.weight"] = {r.freq_emb_rows, c.channels};
+    expect["channel_upsampler.weight"] = {D, P, 1};
+    expect["channel_upsampler.bias"] = {D};
+    expect["channel_upsampler_t.weight"] = {D, P, 1};
+    expect["channel_upsampler_t.bias"] = {D};
+    expect["channel_downsampler.weight"] = {P, D, 1};
+    expect["channel_downsampler.bias"] = {P};
+    expect["channel_downsampler_t.weight"] = {P, D, 1};
+    expect["channel_downsampler_t.bias"] = {P};
+    for (const char *nm : {"crosstransformer.norm_in", "crosstransformer.norm_in_t"}) {
+        expect[std::string(nm) + ".weight"] = {D};
+        expect[std::string(nm) + ".bias"] = {D};
+    }
+    for (int i = 0; i < c.t_layers; ++i)
+        for (const char *branch : {"crosstransformer.layers.", "crosstransformer.layers_t."}) {
+            std::string p = branch + std::to_string(i);
+            bool cross = i % 2 == 1;
+            std::string a = p + (cross ? ".cross_attn" : ".self_attn");
+            expect[a + ".in_proj_weight"] = {3 * D, D};
+            expect[a + ".in_proj_bias"] = {3 * D};
+            expect[a + ".out_proj.weight"] = {D, D};
+            expect[a + ".out_proj.bias"] = {D};
+            expect[p + ".linear1.weight"] = {H, D};
+            expect[p + ".linear1.bias"] = {H};
+            expect[p + ".linear2.weight"] = {D, H};
+            expect[p + ".linear2.bias"] = {D};
+            std::vector<std::string> norms = {".norm1", ".norm2", ".norm_out"};
+            if (cross) norms.push_back(".norm3");
+            for (auto &nm : norms) {
+                expect[p + nm + ".weight"] = {D};
+                expect[p + nm + ".bias"] = {D};
+            }
+            expect[p + ".gamma_1.scale"] = {D};
+            expect[p + ".gamma_2.scale"] = {D};
+        }
+    // Check, then upload every expected tensor into one block.
+    size_t total = 0;
+    for (auto &kv : expect) {
+        auto it = given.find(kv.first);
+        if (it == given.end()) throw_error(DMX_ERR_MISSING_WEIGHT, "weight `" + kv.first + "` not found in checkpoint");
+        const dmx_tensor *t = it->second;
+        std::vector<int64_t> shape(t->shape, t->shape + std::max(0, std::min(4, (int)t->ndim)));
+        if ((int)t->ndim != (int)kv.second.size() || shape != kv.second) {
+            std::string f, e;
+            for (auto v : shape) f += std::to_string(v) + ",";
+            for (auto v : kv.second) e += std::to_string(v) + ",";
+            throw_error(DMX_ERR_WEIGHT_SHAPE, "weight `" + kv.first + "` shape mismatch: checkpoint [" + f +
+                                                  "], model expects [" + e + "]");
+        }
+        int64_t count = 1;
+        for (auto v : kv.second) count *= v;
+        total += ((size_t)count + 63) / 64 * 64;
+    }
+    DMX_HIP(hipMalloc(&r.weight_mem, total * sizeof(float)));
+    float *base = static_cast<float *>(r.weight_mem);
+    size_t off = 0;
+    for (auto &kv : expect) {
+        const dmx_tensor *t = given[kv.first];
+        int64_t count = 1;
+        for (auto v : kv.second) count *= v;
+        DMX_HIP(hipMemcpy(base + off, t->data, (size_t)count * sizeof(float), hipMemcpyHostToDevice));
+        r.w[kv.first] = base + off;
+        off += ((size_t)count + 63) / 64 * 64;
+    }
+    // Derived forms: convT phase packing, scaled frequency embedding.
+    auto packed_convt = [&](const std::string &name, int ic, int oc) {
+        const dmx_tensor *t = given[name];
+        std::vector<float> p((size_t)4 * oc * ic * 2);
+        pack_conv_transpose(t->data, ic, oc, 8, 4, p.data());
+        return upload(r, p);
+    };
+    {
+        const dmx_tensor *t = given["freq_emb.embedding.weight"];
+        std::vector<float> e((size_t)t->shape[0] * t->shape[1]);
+        for (size_t i = 0; i < e.size(); ++i) e[i] = t->data[i] * (float)c.emb_scale;
+        r.freq_emb = upload(r, e);
+    }
+    auto fill_dconv = [&](LayerW &L, const std::string &p, int ch) {
+        for (int d = 0; d < 2; ++d) {
+            std::string at = p + ".layers." + std::to_string(d);
+            L.dconv[d] = {dev(r, at + ".0.weight"), dev(r, at + ".0.bias"), dev(r, at + ".1.weight"),
+                          dev(r, at + ".1.bias"),   dev(r, at + ".3.weight"), dev(r, at + ".3.bias"),
+                          dev(r, at + ".4.weight"), dev(r, at + ".4.bias"), dev(r, at + ".6.scale"),
+                          ch / hidden_div};
+        }
+    };
+    chin = c.audio_channels;
+    chin_z = chin * 2;
+    chout = c.channels;
+    chout_z = c.channels;
+    for (int i = 0; i < depth; ++i) {
+        std::string e = "encoder." + std::to_string(i), te = "tencoder." + std::to_string(i);
+        LayerW L;
+        L.conv_w = dev(r, e + ".conv.weight");
+        L.conv_b = dev(r, e + ".conv.bias");
+        L.rw = dev(r, e + ".rewrite.weight");
+        L.rb = dev(r, e + ".rewrite.bias");
+        L.cin = chin_z;
+        L.cout = chout_z;
+        fill_dconv(L, e + ".dconv", chout_z);
+        r.enc.push_back(L);
+        LayerW T;
+        T.conv_w = dev(r, te + ".conv.weight");
+        T.conv_b = dev(r, te + ".conv.bias");
+        T.rw = dev(r, te + ".rewrite.weight");
+        T.rb = dev(r, te + ".rewrite.bias");
+        T.cin = chin;
+        T.cout = chout;
+        fill_dconv(T, te + ".dconv", chout);
+        r.tenc.push_back(T);
+        chin = chout;
+        chin_z = chout_z;
+        chout *= c.growth;
+        chout_z *= c.growth;
+    }
+    for (int i = depth - 1; i >= 0; --i) {
+        std::string d = "decoder." + std::to_string(i), td = "tdecoder." + std::to_string(i);
+        LayerW L;
+        L.cin = dspec[i].chin;
+        L.cout = dspec[i].chout;
+        L.conv_w = packed_convt(d + ".conv_tr.weight", L.cin, L.cout);
+        L.conv_b = dev(r, d + ".conv_tr.bias");
+        L.rw = dev(r, d + ".rewrite.weight");
+        L.rb = dev(r, d + ".rewrite.bias");
+        fill_dconv(L, d + ".dconv", L.cin);
+        r.dec.push_back(L);
+        LayerW T;
+        T.cin = tdspec[i].chin;
+        T.cout = tdspec[i].chout;
+        T.conv_w = packed_convt(td + ".conv_tr.weight", T.cin, T.cout);
+        T.conv_b = dev(r, td + ".conv_tr.bias");
+        T.rw = dev(r, td + ".rewrite.weight");
+        T.rb = dev(r, td + ".rewrite.bias");
+        fill_dconv(T, td + ".dconv", T.cin);
+        r.tdec.push_back(T);
+    }
+    for (int i = 0; i < c.t_layers; ++i)
+        for (int branch = 0; branch < 2; ++branch) {
+            std::string p = std::string(branch ? "crosstransformer.layers_t." : "crosstransformer.layers.") +
+                            std::to_string(i);
+            TLayerW L{};
+            L.cross = i % 2 == 1;
+            std::string a = p + (L.cross ? ".cross_attn" : ".self_attn");
+            L.in_w = dev(r, a + ".in_proj_weight");
+            L.in_b = dev(r, a + ".in_proj_bias");
+            L.out_w = dev(r, a + ".out_proj.weight");
+            L.out_b = dev(r, a + ".out_proj.bias");
+            L.w1 = dev(r, p + ".linear1.weight");
+            L.b1 = dev(r, p + ".linear1.bias");
+            L.w2 = dev(r, p + ".linear2.weight");
+            L.b2 = dev(r, p + ".linear2.bias");
+            L.n1w = dev(r, p + ".norm1.weight");
+            L.n1b = dev(r, p + ".norm1.bias");
+            L.n2w = dev(r, p + ".norm2.weight");
+            L.n2b = dev(r, p + ".norm2.bias");
+            if (L.cross) {
+                L.n3w = dev(r, p + ".norm3.weight");
+                L.n3b = dev(r, p + ".norm3.bias");
+            }
+            L.now_ = dev(r, p + ".norm_out.weight");
+            L.nob = dev(r, p + ".norm_out.bias");
+            L.g1 = dev(r, p + ".gamma_1.scale");
+            L.g2 = dev(r, p + ".gamma_2.scale");
+            (branch ? r.layers_t : r.layers).push_back(L);
+        }
+    std::vector<float> tw((size_t)c.nfft / 2 * 2 + c.nfft);
+    make_twiddles(c.nfft, tw.data());
+    r.twiddles = upload(r, tw);
+}
+
+void set_device(const dmx_runner *r) { DMX_HIP(hipSetDevice(r->device)); }
+
+// ----- separation (chunk loop on device) -----
+
+struct ShiftRng {
+    uint64_t s;
+    explicit ShiftRng(uint64_t seed) : s(seed * 6364136223846793005ULL + 1ULL) {}
+    int64_t randint(int64_t max) {
+        s = s * 6364136223846793005ULL + 1442695040888963407ULL;
+        return (int64_t)((s >> 33) % (uint64_t)(max + 1));
+    }
+};
+
+float *ola_weight_for(dmx_runner &r, int64_t seg, double power) {
+    auto it = r.ola_weights.find(seg);
+    if (it != r.ola_weights.end() && power == 1.0) return it->second;
+    float *p = upload(r, transition_weight(seg, power));
+    if (power == 1.0) r.ola_weights[seg] = p;
+    return p;
+}
+
+void separate_device(dmx_runner *const *nets, const float *bag_weights, int n_nets, const uint8_t *wanted,
+                     const float *mix, int64_t samples, int sample_rate, const dmx_separate_options &o,
+                     dmx_progress_fn progress, void *user, float *stems) {
+    if (n_nets < 1 || !nets || !nets[0]) throw_error(DMX_ERR_ARGUMENT, "no network");
+    dmx_runner &r0 = *nets[0];
+    for (int i = 0; i < n_nets; ++i) {
+        if (!nets[i]) throw_error(DMX_ERR_ARGUMENT, "null network in the bag");
+        if (nets[i]->device != r0.device) throw_error(DMX_ERR_ARGUMENT, "bag networks must share one device");
+        if (nets[i]->cfg.sources != r0.cfg.sources || nets[i]->cfg.samplerate != r0.cfg.samplerate)
+            throw_error(DMX_ERR_CONFIG, "bag networks disagree on sources or sample rate");
+    }
+    if (sample_rate != r0.cfg.samplerate)
+        throw_error(DMX_ERR_SHAPE, "audio is at " + std::to_string(sample_rate) + " Hz but the model wants " +
+                                       std::to_string(r0.cfg.samplerate) + " Hz");
+    if (samples <= 0) throw_error(DMX_ERR_SHAPE, "empty mix");
+    const int S = r0.cfg.sources, rows = S * 2;
+    hipStream_t s = r0.stream;
+    const double seg_s = o.segment > 0 ? o.segment : r0.cfg.segment;
+    const int64_t seg = (int64_t)((double)r0.cfg.samplerate * seg_s);
+    for (int i = 0; i < n_nets; ++i)
+        if (seg > nets[i]->training_length) throw_error(DMX_ERR_SHAPE, "segment longer than the model's");
+    const int64_t stride = (int64_t)((1.0 - o.overlap) * (double)seg);
+    if (stride == 0) throw_error(DMX_ERR_SHAPE, "overlap leaves a zero stride");
+    const int group = std::max(1, std::min(o.batch_chunks, 64));
+    std::vector<uint8_t> requested(S, 1);
+    if (wanted)
+        for (int i = 0; i < S; ++i) requested[i] = wanted[i] != 0;
+    const bool bag = bag_weights != nullptr;
+    std::vector<int> active;
+    for (int n = 0; n < n_nets; ++n) {
+        if (!bag) {
+            if (n == 0) active.push_back(0);
+            continue;
+        }
+        bool needed = false;
+        for (int i = 0; i < S; ++i) needed |= bag_weights[n * S + i] != 0.0f && requested[i];
+        if (needed) active.push_back(n);
+    }
+    if (active.empty()) throw_error(DMX_ERR_SHAPE, "no network covers any requested stem");
+    std::vector<float> totals(S, 0.0f);
+    if (bag) {
+        for (int n : active)
+            for (int i = 0; i < S; ++i)
+                if (bag_weights[n * S + i] != 0.0f && requested[i]) totals[i] += bag_weights[n * S + i];
+        for (int i = 0; i < S; ++i)
+            if (requested[i] && totals[i] == 0.0f)
+                throw_error(DMX_ERR_SHAPE, "no network covers stem index " + std::to_string(i));
+    }
+    // Per-net masked weights and the totals, on device.
+    DBuf d_w = fbuf(s, (int64_t)n_nets * S), d_tot = fbuf(s, S);
+    std::vector<float> masked(n_nets * S, 0.0f);
+    if (bag)
+        for (int n = 0; n < n_nets; ++n)
+            for (int i = 0; i < S; ++i) masked[n * S + i] = requested[i] ? bag_weights[n * S + i] : 0.0f;
+    DMX_HIP(hipMemcpyAsync(d_w.p, masked.data(), masked.size() * sizeof(float), hipMemcpyHostToDevice, s));
+    DMX_HIP(hipMemcpyAsync(d_tot.p, totals.data(), totals.size() * sizeof(float), hipMemcpyHostToDevice, s));
+    DBuf d_mask(s, S);
+    DMX_HIP(hipMemcpyAsync(d_mask.p, requested.data(), S, hipMemcpyHostToDevice, s));
+
+    DBuf stats = dbuf(s, 2);
+    mix_moments(s, mix, samples, stats.d());
+    const float *weight = ola_weight_for(r0, seg, o.transition_power);
+    const int64_t max_shift = (int64_t)(0.5 * (double)r0.cfg.samplerate);
+    ShiftRng rng(0x5eed1234ULL);
+    const int shifts = std::max(0, o.shifts);
+    const int passes = std::max(1, shifts);
+    // Progress: chunks per pass x passes x active networks.
+    auto chunks_in = [&](int64_t view_len) { return (view_len + stride - 1) / stride; };
+    size_t total = 0;
+    {
+        ShiftRng probe(0x5eed1234ULL);
+        for (int p = 0; p < passes; ++p) {
+            int64_t vl = shifts == 0 ? samples : samples + max_shift - probe.randint(max_shift);
+            total += (size_t)chunks_in(vl) * active.size();
+        }
+    }
+    size_t done = 0;
+    const float scale = shifts > 0 ? 1.0f / (float)shifts : 1.0f;
+    if (shifts > 1) {
+        // stems accumulates the passes; clear the wanted rows first.
+        for (int i = 0; i < S; ++i)
+            if (requested[i]) zero_floats(s, stems + (int64_t)i * 2 * samples, 2 * samples);
+    }
+    for (int pass = 0; pass < passes; ++pass) {
+        int64_t offset = 0, view_len = samples, trim = 0, mshift = 0;
+        if (shifts > 0) {
+            offset = rng.randint(max_shift);
+            trim = max_shift - offset;
+            view_len = samples + max_shift - offset;
+            mshift = max_shift;
+        }
+        DBuf acc = fbuf(s, (int64_t)rows * view_len), sum_w = fbuf(s, view_len);
+        zero_floats(s, acc.f(), (int64_t)rows * view_len);
+        zero_floats(s, sum_w.f(), view_len);
+        DBuf chunk = fbuf(s, (int64_t)group * 2 * seg);
+        DBuf out = fbuf(s, (int64_t)group * rows * seg);
+        DBuf one = bag ? fbuf(s, (int64_t)group * rows * seg) : DBuf();
+        for (int64_t cursor = 0; cursor < view_len;) {
+            std::vector<int64_t> starts, lens;
+            while ((int)starts.size() < group && cursor < view_len) {
+                starts.push_back(cursor);
+                lens.push_back(std::min(view_len - cursor, seg));
+                cursor += stride;
+            }
+            const int g = (int)starts.size();
+            build_chunks(s, mix, samples, stats.d(), g, starts.data(), lens.data(), seg, view_len, offset, mshift,
+                         chunk.f());
+            if (!bag) {
+                forward_device(r0, s, chunk.f(), g, 2, seg, out.f());
+            } else {
+                zero_floats(s, out.f(), (int64_t)g * rows * seg);
+                for (int n : active) {
+                    forward_device(*nets[n], s, chunk.f(), g, 2, seg, one.f());
+                    bag_accumulate(s, one.f(), g, S, 2 * seg, d_w.f() + n * S, out.f(), 0);
+                }
+                bag_divide(s, out.f(), g, S, 2 * seg, d_tot.f());
+            }
+            ola_accumulate(s, out.f(), g, starts.data(), lens.data(), seg, rows, view_len, weight, acc.f(), sum_w.f());
+            done += (size_t)g * active.size();
+            if (progress) {
+                DMX_HIP(hipStreamSynchronize(s));
+                progress(done, total, user);
+            }
+        }
+        const int mode = shifts > 1 ? 1 : 0;
+        ola_finish(s, acc.f(), sum_w.f(), rows, view_len, trim, samples, stats.d(), scale, mode, stems,
+                   static_cast<const uint8_t *>(d_mask.p));
+    }
+    if (shifts > 1)
+        ola_finish(s, nullptr, nullptr, rows, 0, 0, samples, stats.d(), scale, 2, stems,
+                   static_cast<const uint8_t *>(d_mask.p));
+}
+
+}  // namespace
+}  // namespace dmx
+
+namespace dmx {
+std::string &last_error_slot() {
+    static thread_local std::string slot;
+    return slot;
+}
+}  // namespace dmx
+
+using namespace dmx;
+
+extern "C" {
+
+void dmx_config_default(dmx_config *c) {
+    if (!c) return;
+    c->sources = 4;
+    c->audio_channels = 2;
+    c->samplerate = 44100;
+    c->segment = 39.0 / 5.0;
+    c->channels = 48;
+    c->growth = 2;
+    c->nfft = 4096;
+    c->depth = 4;
+    c->stride = 4;
+    c->kernel_size = 8;
+    c->context = 1;
+    c->freq_emb = 0.2;
+    c->emb_scale = 10.0;
+    c->cac = 1;
+    c->bottom_channels = 512;
+    c->t_layers = 5;
+    c->t_heads = 8;
+    c->t_hidden_scale = 4.0;
+    c->t_max_period = 10000.0;
+    c->t_weight_pos_embed = 1.0;
+}
+
+int64_t dmx_config_training_length(const dmx_config *c) {
+    return c ? (int64_t)(c->segment * (double)c->samplerate) : 0;
+}
+
+const char *dmx_last_error(void) { return last_error_slot().c_str(); }
+
+int dmx_device_count(void) {
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess) return 0;
+    return n;
+}
+
+int dmx_runner_create(const dmx_tensor *weights, size_t n_weights, const dmx_config *cfg, int device_ordinal,
+                      int precision, dmx_runner **out) {
+    if (!out) {
+        last_error_slot() = "null output pointer";
+        return DMX_ERR_ARGUMENT;
+    }
+    *out = nullptr;
+    std::unique_ptr<dmx_runner> r(new dmx_runner());
+    int rc = guarded([&] {
+        if (!weights || !cfg) throw_error(DMX_ERR_ARGUMENT, "null weights or config");
+        if (precision != DMX_PRECISION_FP32 && precision != DMX_PRECISION_BF16)
+            throw_error(DMX_ERR_ARGUMENT, "unknown precision");
+        if (precision == DMX_PRECISION_BF16)
+            throw_error(DMX_ERR_UNSUPPORTED, "the bf16 MFMA variant is not built yet");
+        validate(*cfg);
+        int count = 0;
+        if (hipGetDeviceCount(&count) != hipSuccess || count == 0) throw_error(DMX_ERR_GPU, "no HIP device is visible");
+        if (device_ordinal < 0 || device_ordinal >= count)
+            throw_error(DMX_ERR_GPU, "device ordinal " + std::to_string(device_ordinal) + " out of range");
+        r->cfg = *cfg;
+        r->device = device_ordinal;
+        r->precision = precision;
+        r->training_length = dmx_config_training_length(cfg);
+        r->hop = cfg->nfft / 4;
+        DMX_HIP(hipSetDevice(device_ordinal));
+        hipDeviceProp_t prop;
+        DMX_HIP(hipGetDeviceProperties(&prop, device_ordinal));
+        r->tag = std::string("hip:") + prop.name + ":" + prop.gcnArchName;
+        DMX_HIP(hipStreamCreateWithFlags(&r->stream, hipStreamNonBlocking));
+        hipMemPool_t pool;
+        if (hipDeviceGetDefaultMemPool(&pool, device_ordinal) == hipSuccess) {
+            uint64_t threshold = UINT64_MAX;
+            (void)hipMemPoolSetAttribute(pool, hipMemPoolAttrReleaseThreshold, &threshold);
+        }
+        load_weights(*r, weights, n_weights);
+    });
+    if (rc != DMX_OK) {
+        if (r->stream) (void)hipStreamDestroy(r->stream);
+        if (r->weight_mem) (void)hipFree(r->weight_mem);
+        for (void *p : r->owned) (void)hipFree(p);
+        return rc;
+    }
+    *out = r.release();
+    return DMX_OK;
+}
+
+void dmx_runner_destroy(dmx_runner *r) {
+    if (!r) return;
+    (void)hipSetDevice(r->device);
+    if (r->stream) (void)hipStreamSynchronize(r->stream);
+    if (r->weight_mem) (void)hipFree(r->weight_mem);
+    for (void *p : r->owned) (void)hipFree(p);
+    if (r->stream) (void)hipStreamDestroy(r->stream);
+    delete r;
+}
+
+const char *dmx_runner_backend_tag(const dmx_runner *r) { return r ? r->tag.c_str() : ""; }
+void *dmx_runner_stream(dmx_runner *r) { return r ? (void *)r->stream : nullptr; }
+
+int dmx_synchronize(dmx_runner *r) {
+    return guarded([&] {
+        if (!r) throw_error(DMX_ERR_ARGUMENT, "null runner");
+        set_device(r);
+        DMX_HIP(hipStreamSynchronize(r->stream));
+    });
+}
+
+int dmx_set_trace(dmx_runner *r, dmx_trace_wants_fn wants, dmx_trace_record_fn record, void *user) {
+    return guarded([&] {
+        if (!r) throw_error(DMX_ERR_ARGUMENT, "null runner");
+        r->trace = Trace{wants, record, user};
+    });
+}
+
+int dmx_forward_device(dmx_runner *r, const float *d_mix, int64_t batch, int64_t channels, int64_t length,
+                       float *d_stems) {
+    return guarded([&] {
+        if (!r || !d_mix || !d_stems) throw_error(DMX_ERR_ARGUMENT, "null argument");
+        set_device(r);
+        forward_device(*r, r->stream, d_mix, batch, channels, length, d_stems);
+    });
+}
+
+int dmx_forward_start(dmx_runner *r, const float *mix, int64_t batch, int64_t channels, int64_t length,
+                      dmx_pending **out) {
+    if (out) *out = nullptr;
+    std::unique_ptr<dmx_pending> p(new dmx_pending());
+    int rc = guarded([&] {
+        if (!r || !mix || !out) throw_error(DMX_ERR_ARGUMENT, "null argument");
+        set_device(r);
+        if (channels != r->cfg.audio_channels) throw_error(DMX_ERR_SHAPE, "wrong audio channel count");
+        if (batch <= 0 || length <= 0 || length > r->training_length)
+            throw_error(DMX_ERR_SHAPE, "input must hold 1..training_length samples per channel");
+        hipStream_t s = r->stream;
+        const size_t in_n = (size_t)(batch * channels * length);
+        const size_t out_n = (size_t)(batch * r->cfg.sources * channels * length);
+        DMX_HIP(hipHostMalloc((void **)&p->host_in, in_n * sizeof(float), hipHostMallocDefault));
+        std::memcpy(p->host_in, mix, in_n * sizeof(float));
+        DMX_HIP(hipHostMalloc((void **)&p->host_out, out_n * sizeof(float), hipHostMallocDefault));
+        p->count = out_n;
+        DBuf d_in(s, in_n * sizeof(float)), d_out(s, out_n * sizeof(float));
+        DMX_HIP(hipMemcpyAsync(d_in.p, p->host_in, in_n * sizeof(float), hipMemcpyHostToDevice, s));
+        forward_device(*r, s, d_in.f(), batch, channels, length, d_out.f());
+        DMX_HIP(hipMemcpyAsync(p->host_out, d_out.p, out_n * sizeof(float), hipMemcpyDeviceToHost, s));
+        DMX_HIP(hipEventCreateWithFlags(&p->done, hipEventDisableTiming));
+        DMX_HIP(hipEventRecord(p->done, s));
+        // Both staging buffers belong to the pending group until collect.
+    });
+    if (rc != DMX_OK) {
+        if (p->done) (void)hipEventSynchronize(p->done);
+        if (p->host_in) (void)hipHostFree(p->host_in);
+        if (p->host_out) (void)hipHostFree(p->host_out);
+        if (p->done) (void)hipEventDestroy(p->done);
+        return rc;
+    }
+    *out = p.release();
+    return DMX_OK;
+}
+
+int dmx_forward_collect(dmx_runner *r, dmx_pending *p, float *stems) {
+    int rc = guarded([&] {
+        if (!r || !p || !stems) throw_error(DMX_ERR_ARGUMENT, "null argument");
+        set_device(r);
+        DMX_HIP(hipEventSynchronize(p->done));
+        std::memcpy(stems, p->host_out, p->count * sizeof(float));
+    });
+    if (p) {
+        if (p->done) (void)hipEventSynchronize(p->done);
+        if (p->host_in) (void)hipHostFree(p->host_in);
+        if (p->host_out) (void)hipHostFree(p->host_out);
+        if (p->done) (void)hipEventDestroy(p->done);
+        delete p;
+    }
+    return rc;
+}
+
+int dmx_forward(dmx_runner *r, const float *mix, int64_t batch, int64_t channels, int64_t length, float *stems) {
+    dmx_pending *p = nullptr;
+    int rc = dmx_forward_start(r, mix, batch, channels, length, &p);
+    if (rc != DMX_OK) return rc;
+    return dmx_forward_collect(r, p, stems);
+}
+
+int dmx_crosstransformer_device(dmx_runner *r, const float *d_spec, const float *d_time, int64_t batch, int64_t freqs,
+                                int64_t frames, int64_t time_len, float *d_spec_out, float *d_time_out) {
+    return guarded([&] {
+        if (!r || !d_spec || !d_time || !d_spec_out || !d_time_out) throw_error(DMX_ERR_ARGUMENT, "null argument");
+        if (batch <= 0 || freqs <= 0 || frames <= 0 || time_len <= 0) throw_error(DMX_ERR_SHAPE, "empty input");
+        set_device(r);
+        transformer_only(*r, r->stream, d_spec, d_time, (int)batch, (int)freqs, (int)frames, (int)time_len,
+                         d_spec_out, d_time_out);
+    });
+}
+
+void dmx_separate_options_default(dmx_separate_options *o) {
+    if (!o) return;
+    o->shifts = 1;
+    o->overlap = 0.25;
+    o->transition_power = 1.0;
+    o->segment = 0.0;
+    o->batch_chunks = 1;
+}
+
+int dmx_separate_device(dmx_runner *const *nets, const float *bag_weights, int32_t n_nets, const uint8_t *stems_wanted,
+                        const float *d_mix, int64_t samples, int32_t sample_rate, const dmx_separate_options *opts,
+                        dmx_progress_fn progress, void *user, float *d_stems) {
+    return guarded([&] {
+        if (!nets || !d_mix || !d_stems) throw_error(DMX_ERR_ARGUMENT, "null argument");
+        dmx_separate_options o;
+        dmx_separate_options_default(&o);
+        if (opts) o = *opts;
+        set_device(nets[0]);
+        separate_device(nets, bag_weights, n_nets, stems_wanted, d_mix, samples, sample_rate, o, progress, user,
+                        d_stems);
+    });
+}
+
+int dmx_separate(dmx_runner *const *nets, const float *bag_weights, int32_t n_nets, const uint8_t *stems_wanted,
+                 const float *left, const float *right, int64_t samples, int32_t sample_rate,
+                 const dmx_separate_options *opts, dmx_progress_fn progress, void *user, float *stems_out) {
+    return guarded([&] {
+        if (!nets || !nets[0] || !left || !right || !stems_out) throw_error(DMX_ERR_ARGUMENT, "null argument");
+        dmx_separate_options o;
+        dmx_separate_options_default(&o);
+        if (opts) o = *opts;
+        dmx_runner &r = *nets[0];
+        set_device(&r);
+        hipStream_t s = r.stream;
+        const int S = r.cfg.sources;
+        DBuf mix = fbuf(s, 2 * samples), stems = fbuf(s, (int64_t)S * 2 * samples);
+        DMX_HIP(hipMemcpyAsync(mix.f(), left, samples * sizeof(float), hipMemcpyHostToDevice, s));
+        DMX_HIP(hipMemcpyAsync(mix.f() + samples, right, samples * sizeof(float), hipMemcpyHostToDevice, s));
+        separate_device(nets, bag_weights, n_nets, stems_wanted, mix.f(), samples, sample_rate, o, progress, user,
+                        stems.f());
+        for (int i = 0; i < S; ++i) {
+            if (stems_wanted && !stems_wanted[i]) continue;
+            DMX_HIP(hipMemcpyAsync(stems_out + (int64_t)i * 2 * samples, stems.f() + (int64_t)i * 2 * samples,
+                                   2 * samples * sizeof(float), hipMemcpyDeviceToHost, s));
+        }
+        DMX_HIP(hipStreamSynchronize(s));
+    });
+}
+
+}  // extern "C"

@@ -1,0 +1,111 @@
+"""End-to-end parity of the HIP forward against the CPU oracle: per-stem SNR
+>= 60 dB and per-named-activation max |err| <= 1e-3 (fp32), on seeded inputs
+and random-init weights; plus the SegmentForward contract (two groups in
+flight, batch independence) and the error paths the C-ABI must raise.
+"""
+import numpy as np
+import pytest
+
+from conftest import small_config, snr_db
+
+pytestmark = pytest.mark.gpu
+
+TRACED = ["x_normalized", "xt_normalized", "tencoder.0", "tencoder.3", "encoder.1", "encoder.3",
+          "channel_upsampler", "crosstransformer.layers.0", "crosstransformer.layers_t.1",
+          "crosstransformer.layers.4", "channel_downsampler", "decoder.0#0", "tdecoder.2#0", "decoder.3#0",
+          "tdecoder.3#0", "model_out"]
+
+
+@pytest.fixture(scope="module")
+def small(dmx, oracle):
+    cfg = small_config(dmx, 11025)
+    weights = dmx.random_init(0, cfg)
+    return cfg, weights, dmx.Runner(weights, cfg), oracle.Model(weights, cfg)
+
+
+def per_stem_snr(ref, out):
+    return [snr_db(ref[:, s], out[:, s]) for s in range(ref.shape[1])]
+
+
+def test_forward_matches_oracle_per_stem_and_per_activation(dmx, small):
+    cfg, weights, runner, model = small
+    mix = dmx.signals.gaussian_segments(0, 2, cfg.training_length)
+    ref_trace, gpu_trace = {}, {}
+    wants = lambda name: name in TRACED
+    ref = model.forward(mix, ref_trace, wants)
+    runner.set_trace(wants, lambda n, a: gpu_trace.__setitem__(n, a))
+    try:
+        out = runner.forward(mix)
+    finally:
+        runner.set_trace(None, None)
+    snrs = per_stem_snr(ref, out)
+    assert min(snrs) >= 60.0, snrs
+    for name in TRACED:
+        assert name in gpu_trace and name in ref_trace, name
+        a, b = ref_trace[name], gpu_trace[name]
+        assert a.shape == b.shape, (name, a.shape, b.shape)
+        err = float(np.max(np.abs(a - b)))
+        assert err <= 1e-3 * max(1.0, float(np.max(np.abs(a)))), (name, err)
+
+
+def test_shorter_input_is_padded_and_trimmed(dmx, small):
+    cfg, weights, runner, model = small
+    mix = dmx.signals.gaussian_segments(3, 1, 9000)
+    ref = model.forward(mix)
+    out = runner.forward(mix)
+    assert out.shape == (1, 4, 2, 9000)
+    assert min(per_stem_snr(ref, out)) >= 60.0
+
+
+def test_batch_elements_are_independent(dmx, small):
+    cfg, weights, runner, model = small
+    mix = dmx.signals.gaussian_segments(1, 2, cfg.training_length)
+    both = runner.forward(mix)
+    one = runner.forward(mix[1:2])
+    assert snr_db(one[0], both[1]) > 100.0  # core/tests/demucs_alignment.rs:231-261
+
+
+def test_two_groups_in_flight(dmx, small):
+    cfg, weights, runner, model = small
+    a = dmx.signals.gaussian_segments(4, 1, cfg.training_length)
+    b = dmx.signals.gaussian_segments(5, 2, cfg.training_length)
+    pa = runner.start(a)
+    pb = runner.start(b)  # queued before `a` is collected
+    out_a, out_b = runner.collect(pa), runner.collect(pb)
+    np.testing.assert_array_equal(out_a, runner.forward(a))
+    np.testing.assert_array_equal(out_b, runner.forward(b))
+
+
+def test_shape_errors_are_reported(dmx, small):
+    cfg, weights, runner, model = small
+    with pytest.raises(dmx.DmxError) as e:
+        runner.forward(np.zeros((1, 2, cfg.training_length + 1), np.float32))
+    assert e.value.kind == "Shape"
+    with pytest.raises(dmx.DmxError) as e:
+        runner.forward(np.zeros((1, 3, 100), np.float32))
+    assert e.value.kind == "Shape"
+
+
+def test_missing_and_misshapen_weights_are_reported(dmx, small):
+    cfg, weights, runner, model = small
+    w = dict(weights)
+    del w["encoder.2.rewrite.bias"]
+    with pytest.raises(dmx.DmxError) as e:
+        dmx.Runner(w, cfg)
+    assert e.value.kind == "MissingWeight"
+    w = dict(weights)
+    w["decoder.1.conv_tr.weight"] = np.zeros((1, 2, 3), np.float32)
+    with pytest.raises(dmx.DmxError) as e:
+        dmx.Runner(w, cfg)
+    assert e.value.kind == "WeightShape"
+
+
+def test_full_segment_forward_matches_oracle(dmx, oracle):
+    """one 7.8 s segment, seed-0 weights, N(0, 0.1^2) input."""
+    cfg = dmx.Config()
+    weights = dmx.random_init(0, cfg)
+    mix = dmx.signals.gaussian_segments(0, 1, cfg.training_length)
+    out = dmx.Runner(weights, cfg).forward(mix)
+    ref = oracle.Model(weights, cfg).forward(mix)
+    snrs = per_stem_snr(ref, out)
+    assert min(snrs) >= 60.0, snrs

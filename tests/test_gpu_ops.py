@@ -1,0 +1,277 @@
+"""Per-kernel parity: each HIP kernel through include/dmx_ops.h against the CPU
+oracle on the same seeded inputs, at the reference's own gates
+(core/tests/gpu_*.rs): rms-relative <= 1e-5 for contractions, <= 1e-6 for
+norms/elementwise (relaxed where noted for the f32 FFT), exact for data movement.
+"""
+import ctypes
+
+import numpy as np
+import pytest
+
+from conftest import rms_relative_error, snr_db
+
+pytestmark = pytest.mark.gpu
+
+torch = pytest.importorskip("torch")
+
+
+def rng(seed):
+    return np.random.default_rng(seed)
+
+
+def dev(a):
+    return torch.from_numpy(np.ascontiguousarray(a, dtype=np.float32)).cuda()
+
+
+def ptr(t):
+    return ctypes.c_void_p(0 if t is None else t.data_ptr())
+
+
+def stream():
+    return ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+
+@pytest.fixture(scope="module")
+def lib(dmx):
+    from demucs_wgpu_amd import _native
+    return _native.load()
+
+
+def call(lib, name, *args):
+    rc = getattr(lib, name)(*args)
+    torch.cuda.synchronize()
+    if rc != 0:
+        raise RuntimeError(f"{name}: {lib.dmx_last_error().decode()}")
+
+
+@pytest.mark.parametrize("rows,k,n,tail", [(300, 512, 1536, 0), (37, 19, 70, 0), (64, 512, 2048, 1),
+                                           (129, 2048, 512, 2), (2688, 512, 512, 2)])
+def test_linear_matches_oracle(lib, oracle, rows, k, n, tail):
+    r = rng(rows + k + n)
+    x = r.uniform(-0.4, 0.4, (rows, k)).astype(np.float32)
+    w = r.uniform(-0.4, 0.4, (n, k)).astype(np.float32)
+    b = r.uniform(-0.4, 0.4, n).astype(np.float32)
+    res = r.uniform(-1, 1, (rows, n)).astype(np.float32)
+    g = r.uniform(0.1, 0.5, n).astype(np.float32)
+    ref = oracle.sgemm(x, w.T) + b
+    if tail == 1:
+        ref = oracle.gelu(ref)
+    elif tail == 2:
+        ref = res + ref * g
+    dx, dw, db, dres, dg = dev(x), dev(w), dev(b), dev(res), dev(g)
+    out = torch.empty((rows, n), device="cuda")
+    call(lib, "dmx_op_linear", stream(), ptr(dx), rows, k, ptr(dw), ptr(db), n, tail, ptr(dres), ptr(dg), ptr(out))
+    assert rms_relative_error(ref, out.cpu().numpy()) < 1e-5
+
+
+@pytest.mark.parametrize("b,ic,h,w,oc,kh,kw,sh,sw,ph,pw,dh,dw", [
+    (1, 4, 64, 9, 48, 8, 1, 4, 1, 2, 0, 1, 1),      # freq encoder conv (k(8,1) s(4,1) p(2,0))
+    (2, 2, 1, 203, 48, 1, 8, 1, 4, 0, 2, 1, 1),     # time encoder conv
+    (1, 24, 16, 11, 48, 3, 3, 1, 1, 1, 1, 1, 1),    # decoder 3x3 rewrite
+    (2, 12, 1, 77, 6, 1, 3, 1, 1, 0, 2, 1, 2),      # DConv conv1, dilation 2
+    (1, 5, 7, 13, 130, 1, 1, 1, 1, 0, 0, 1, 1),     # 1x1, M > 128 (two m-tiles)
+    (1, 3, 9, 10, 7, 2, 3, 2, 3, 1, 2, 2, 1),       # generic kernel path
+])
+def test_conv2d_matches_oracle(lib, oracle, b, ic, h, w, oc, kh, kw, sh, sw, ph, pw, dh, dw):
+    r = rng(ic * 31 + oc)
+    x = r.uniform(-0.4, 0.4, (b, ic, h, w)).astype(np.float32)
+    wt = r.uniform(-0.4, 0.4, (oc, ic, kh, kw)).astype(np.float32)
+    bias = r.uniform(-0.4, 0.4, oc).astype(np.float32)
+    ref = oracle.conv2d(x, wt, bias, (sh, sw), (ph, pw), (dh, dw))
+    out = torch.empty(ref.shape, device="cuda")
+    dx, dwt, dbias = dev(x), dev(wt), dev(bias)
+    call(lib, "dmx_op_conv2d", stream(), ptr(dx), None, b, ic, h, w, ptr(dwt), ptr(dbias), oc, kh, kw, sh, sw, ph,
+         pw, dh, dw, 0, ptr(out))
+    assert rms_relative_error(ref, out.cpu().numpy()) < 1e-5
+
+
+def test_conv2d_gelu_and_skip(lib, oracle):
+    r = rng(5)
+    x = r.uniform(-1, 1, (2, 8, 12, 10)).astype(np.float32)
+    s = r.uniform(-1, 1, x.shape).astype(np.float32)
+    wt = r.uniform(-0.4, 0.4, (16, 8, 3, 3)).astype(np.float32)
+    bias = r.uniform(-0.4, 0.4, 16).astype(np.float32)
+    ref = oracle.gelu(oracle.conv2d(x + s, wt, bias, (1, 1), (1, 1)))
+    out = torch.empty(ref.shape, device="cuda")
+    dx, ds, dwt, db = dev(x), dev(s), dev(wt), dev(bias)
+    call(lib, "dmx_op_conv2d", stream(), ptr(dx), ptr(ds), 2, 8, 12, 10, ptr(dwt), ptr(db), 16, 3, 3, 1, 1, 1, 1,
+         1, 1, 1, ptr(out))
+    assert rms_relative_error(ref, out.cpu().numpy()) < 1e-5
+
+
+@pytest.mark.parametrize("b,ic,h,w,C,kh,kw", [(1, 48, 32, 12, 48, 1, 1), (2, 24, 1, 300, 24, 1, 3),
+                                               (1, 16, 10, 9, 16, 3, 3), (1, 96, 4, 7, 96, 1, 1)])
+def test_conv2d_glu_matches_oracle(lib, oracle, b, ic, h, w, C, kh, kw):
+    r = rng(C + kh)
+    x = r.uniform(-0.4, 0.4, (b, ic, h, w)).astype(np.float32)
+    wt = r.uniform(-0.4, 0.4, (2 * C, ic, kh, kw)).astype(np.float32)
+    bias = r.uniform(-0.4, 0.4, 2 * C).astype(np.float32)
+    ref = oracle.glu(oracle.conv2d(x, wt, bias, (1, 1), (kh // 2, kw // 2)))
+    out = torch.empty(ref.shape, device="cuda")
+    dx, dwt, db = dev(x), dev(wt), dev(bias)
+    call(lib, "dmx_op_conv2d_glu", stream(), ptr(dx), None, b, ic, h, w, ptr(dwt), ptr(db), C, kh, kw, kh // 2,
+         kw // 2, None, ctypes.c_float(0.0), ptr(out))
+    assert rms_relative_error(ref, out.cpu().numpy()) < 1e-5
+
+
+def test_conv2d_glu_adds_the_frequency_embedding(lib, oracle):
+    r = rng(9)
+    b, ic, f, t, C = 1, 48, 16, 5, 48
+    x = r.uniform(-0.4, 0.4, (b, ic, f, t)).astype(np.float32)
+    wt = r.uniform(-0.4, 0.4, (2 * C, ic, 1, 1)).astype(np.float32)
+    bias = r.uniform(-0.4, 0.4, 2 * C).astype(np.float32)
+    emb = r.normal(0, 1, (f, C)).astype(np.float32)
+    ref = oracle.glu(oracle.conv2d(x, wt, bias)) + (np.float32(0.2) * emb.T)[None, :, :, None]
+    out = torch.empty(ref.shape, device="cuda")
+    dx, dwt, db, de = dev(x), dev(wt), dev(bias), dev(emb)
+    call(lib, "dmx_op_conv2d_glu", stream(), ptr(dx), None, b, ic, f, t, ptr(dwt), ptr(db), C, 1, 1, 0, 0, ptr(de),
+         ctypes.c_float(0.2), ptr(out))
+    assert rms_relative_error(ref, out.cpu().numpy()) < 1e-5
+
+
+@pytest.mark.parametrize("b,ic,A,P,oc,last", [(1, 48, 32, 11, 16, True), (2, 96, 8, 5, 48, False),
+                                              (1, 48, 301, 1, 8, True), (2, 24, 50, 1, 12, False)])
+def test_conv_transpose_matches_oracle(lib, oracle, b, ic, A, P, oc, last):
+    r = rng(ic + A)
+    x = r.uniform(-0.4, 0.4, (b, ic, A, P)).astype(np.float32)
+    wt = r.uniform(-0.4, 0.4, (ic, oc, 8, 1)).astype(np.float32)
+    bias = r.uniform(-0.4, 0.4, oc).astype(np.float32)
+    full = oracle.conv_transpose2d(x, wt, bias, (4, 1))
+    a_out = 4 * A if P > 1 else 4 * A - 1  # the waveform crop keeps `length` <= produced - 2
+    ref = full[:, :, 2:2 + a_out, :]
+    if not last:
+        ref = oracle.gelu(ref)
+    out = torch.empty(ref.shape, device="cuda")
+    dx, dw, db = dev(x), dev(wt.reshape(ic, oc, 8)), dev(bias)
+    call(lib, "dmx_op_conv_transpose", stream(), ptr(dx), b, ic, A, P, ptr(dw), ptr(db), oc, 8, 4, 2, a_out,
+         0 if last else 1, ptr(out))
+    assert rms_relative_error(ref, out.cpu().numpy()) < 1e-5
+
+
+@pytest.mark.parametrize("B,C,F,T", [(1, 48, 16, 40), (2, 96, 1, 700), (1, 384, 2, 33)])
+def test_dconv_matches_oracle(lib, oracle, dmx, B, C, F, T):
+    r = rng(C + T)
+    hid = C // 8
+    w = {}
+    for d in range(2):
+        at = f"x.layers.{d}"
+        w[f"{at}.0.weight"] = r.uniform(-0.5, 0.5, (hid, C, 3)).astype(np.float32)
+        w[f"{at}.0.bias"] = r.uniform(-0.3, 0.3, hid).astype(np.float32)
+        w[f"{at}.1.weight"] = r.uniform(0.75, 1.25, hid).astype(np.float32)
+        w[f"{at}.1.bias"] = r.uniform(-0.2, 0.2, hid).astype(np.float32)
+        w[f"{at}.3.weight"] = r.uniform(-0.5, 0.5, (2 * C, hid, 1)).astype(np.float32)
+        w[f"{at}.3.bias"] = r.uniform(-0.3, 0.3, 2 * C).astype(np.float32)
+        w[f"{at}.4.weight"] = r.uniform(0.75, 1.25, 2 * C).astype(np.float32)
+        w[f"{at}.4.bias"] = r.uniform(-0.2, 0.2, 2 * C).astype(np.float32)
+        w[f"{at}.6.scale"] = r.uniform(0.1, 0.5, C).astype(np.float32)
+    x = r.uniform(-1, 1, (B, C, F, T)).astype(np.float32)
+    rows = x.transpose(0, 2, 1, 3).reshape(B * F, C, T)
+    ref = oracle.dconv(rows, w, "x").reshape(B, F, C, T).transpose(0, 2, 1, 3)
+    dx = dev(x)
+    dw = {k: dev(v) for k, v in w.items()}
+    for d in range(2):
+        at = f"x.layers.{d}"
+        call(lib, "dmx_op_dconv_layer", stream(), ptr(dx), B, C, F, T, 1 << d, ptr(dw[f"{at}.0.weight"]),
+             ptr(dw[f"{at}.0.bias"]), hid, ptr(dw[f"{at}.1.weight"]), ptr(dw[f"{at}.1.bias"]),
+             ptr(dw[f"{at}.3.weight"]), ptr(dw[f"{at}.3.bias"]), ptr(dw[f"{at}.4.weight"]), ptr(dw[f"{at}.4.bias"]),
+             ptr(dw[f"{at}.6.scale"]))
+    assert rms_relative_error(ref, dx.cpu().numpy()) < 1e-5
+
+
+@pytest.mark.parametrize("batch,heads,nq,nk", [(1, 8, 200, 130), (2, 2, 64, 64), (1, 1, 33, 1), (1, 8, 2688, 1344)])
+def test_attention_matches_oracle(lib, oracle, batch, heads, nq, nk):
+    r = rng(nq + nk)
+    D = heads * 64
+    q = r.uniform(-2, 2, (batch, nq, D)).astype(np.float32)
+    k = r.uniform(-2, 2, (batch, nk, D)).astype(np.float32)
+    v = r.uniform(-2, 2, (batch, nk, D)).astype(np.float32)
+    ref = np.empty_like(q)
+    for b in range(batch):
+        for h in range(heads):
+            sl = slice(64 * h, 64 * h + 64)
+            ref[b, :, sl] = oracle.attention_head(q[b, :, sl], k[b, :, sl], v[b, :, sl], 0.125)
+    out = torch.empty(q.shape, device="cuda")
+    dq, dk, dv = dev(q), dev(k), dev(v)
+    call(lib, "dmx_op_attention", stream(), ptr(dq), ptr(dk), ptr(dv), ptr(out), batch, heads, nq, nk,
+         ctypes.c_float(0.125))
+    assert rms_relative_error(ref, out.cpu().numpy()) < 1e-5
+
+
+def test_layer_norm_matches_oracle(lib, oracle):
+    r = rng(1)
+    x = r.uniform(-3, 3, (333, 512)).astype(np.float32)
+    w, b = r.uniform(0.5, 1.5, 512).astype(np.float32), r.uniform(-1, 1, 512).astype(np.float32)
+    ref = oracle.layer_norm(x, w, b)
+    out = torch.empty(x.shape, device="cuda")
+    dx, dw, db = dev(x), dev(w), dev(b)
+    call(lib, "dmx_op_layer_norm", stream(), ptr(dx), 333, 512, ptr(dw), ptr(db), ptr(out))
+    assert rms_relative_error(ref, out.cpu().numpy()) < 1e-6
+
+
+@pytest.mark.parametrize("b,c,inner,groups", [(2, 8, 1000, 1), (1, 16, 77, 4), (3, 6, 5, 2)])
+def test_group_norm_matches_oracle(lib, oracle, b, c, inner, groups):
+    r = rng(c * inner)
+    x = r.uniform(-3, 3, (b, c, inner)).astype(np.float32)
+    w, bias = r.uniform(0.5, 1.5, c).astype(np.float32), r.uniform(-1, 1, c).astype(np.float32)
+    ref = oracle.group_norm(x, groups, w, bias)
+    out = torch.empty(x.shape, device="cuda")
+    dx, dw, db = dev(x), dev(w), dev(bias)
+    call(lib, "dmx_op_group_norm", stream(), ptr(dx), b, c, inner, groups, ptr(dw), ptr(db), ptr(out))
+    assert rms_relative_error(ref, out.cpu().numpy()) < 1e-6
+
+
+def test_glu_and_gelu_match_oracle(lib, oracle):
+    r = rng(2)
+    x = r.uniform(-6, 6, (2, 10, 333)).astype(np.float32)
+    ref_glu, ref_gelu = oracle.glu(x), oracle.gelu(x)
+    out = torch.empty(ref_glu.shape, device="cuda")
+    out2 = torch.empty(x.shape, device="cuda")
+    dx = dev(x)
+    call(lib, "dmx_op_glu", stream(), ptr(dx), 2, 10, 333, ptr(out))
+    call(lib, "dmx_op_gelu", stream(), ptr(dx), x.size, ptr(out2))
+    assert rms_relative_error(ref_glu, out.cpu().numpy()) < 1e-6
+    assert rms_relative_error(ref_gelu, out2.cpu().numpy()) < 1e-6
+
+
+@pytest.mark.parametrize("b,L", [(1, 11025), (2, 30000)])
+def test_spec_normalise_matches_oracle(lib, oracle, b, L):
+    r = rng(L)
+    mix = r.normal(0, 0.1, (b, 2, L)).astype(np.float32)
+    spec = oracle.spec_cac(mix)
+    xs_ref = np.empty_like(spec)
+    xt_ref = np.empty_like(mix)
+    norms_ref = np.empty((b, 4), np.float32)
+    for i in range(b):
+        m, s = oracle.mean(spec[i]), oracle.std_unbiased(spec[i])
+        mt, st = oracle.mean(mix[i]), oracle.std_unbiased(mix[i])
+        xs_ref[i] = (spec[i] - np.float32(m)) * np.float32(1.0 / (1e-5 + np.float32(s)))
+        xt_ref[i] = (mix[i] - np.float32(mt)) * np.float32(1.0 / (1e-5 + np.float32(st)))
+        norms_ref[i] = (m, s, mt, st)
+    xs = torch.empty(spec.shape, device="cuda")
+    xt = torch.empty(mix.shape, device="cuda")
+    norms = torch.empty((b, 4), device="cuda")
+    dmix = dev(mix)
+    call(lib, "dmx_op_spec_normalise", stream(), ptr(dmix), b, L, ptr(xs), ptr(xt), ptr(norms))
+    np.testing.assert_allclose(norms.cpu().numpy(), norms_ref, rtol=1e-5, atol=1e-7)
+    assert snr_db(xs_ref, xs.cpu().numpy()) > 100  # f32 FFT against the f64 oracle FFT
+    assert rms_relative_error(xt_ref, xt.cpu().numpy()) < 1e-6
+
+
+@pytest.mark.parametrize("b,L", [(1, 11025), (2, 30000)])
+def test_ispec_sum_matches_oracle(lib, oracle, b, L):
+    r = rng(L + 1)
+    le = -(-L // 1024)
+    xs = r.normal(0, 1, (b, 16, 2048, le)).astype(np.float32)
+    xt = r.normal(0, 1, (b, 8, L)).astype(np.float32)
+    norms = np.array([[0.01 * (i + 1), 0.5 + i, -0.02, 0.3] for i in range(b)], np.float32)
+    ref = np.empty((b, 4, 2, L), np.float32)
+    for i in range(b):
+        m, s, mt, st = norms[i]
+        den = (xs[i:i + 1] - np.float32(-m / s)) * np.float32(s)
+        wave = oracle.ispec_cac(den, 4, L)
+        tim = ((xt[i] - np.float32(-mt / st)) * np.float32(st)).reshape(4, 2, L)
+        ref[i] = tim + wave[0]
+    out = torch.empty(ref.shape, device="cuda")
+    dxs, dxt, dn = dev(xs), dev(xt), dev(norms)
+    call(lib, "dmx_op_ispec_sum", stream(), ptr(dxs), ptr(dxt), b, L, ptr(dn), ptr(out))
+    assert snr_db(ref, out.cpu().numpy()) > 100
