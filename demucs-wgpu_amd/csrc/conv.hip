@@ -446,6 +446,7 @@ void dconv_layer(hipStream_t s, float *x, int B, int C, int F, int T, int dil, c
     DMX_REQUIRE(rows <= 65535, "dconv_layer: too many rows for one launch");
     double *st1 = stats, *st2 = stats + 2 * rows;
     zero_doubles(s, stats, 4 * (int64_t)rows);
+    if (dconv_layer_narrow(s, x, B, C, F, T, dil, w1, b1, H, n1w, n1b, w2, b2, n2w, n2b, gamma, hbuf, stats)) return;
     // conv1: k3, dilation dil, padding dil, over t; rows (b, f) as the batch.
     EpConv1 e1;
     e1.y = hbuf;

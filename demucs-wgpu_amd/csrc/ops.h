@@ -49,6 +49,12 @@ void dconv_layer(hipStream_t s, float *x, int B, int C, int F, int T, int dil, c
                  int H, const float *n1w, const float *n1b, const float *w2, const float *b2, const float *n2w,
                  const float *n2b, const float *gamma, float *hbuf, double *stats);
 
+// The same layer with direct VALU kernels for hidden widths where MFMA tiles
+// would be mostly padding (dconv.hip); returns false when it does not apply.
+bool dconv_layer_narrow(hipStream_t s, float *x, int B, int C, int F, int T, int dil, const float *w1,
+                        const float *b1, int H, const float *n1w, const float *n1b, const float *w2, const float *b2,
+                        const float *n2w, const float *n2b, const float *gamma, float *hbuf, double *stats);
+
 // out (z, M, N) = W (M, K) . x (z, K, N) + bias[m]  (1x1 conv / channel mixer).
 void pointwise(hipStream_t s, const float *w, const float *bias, const float *x, int batches, int M, int K, int N,
                float *out, Act act);

@@ -27,14 +27,80 @@ namespace dmx {
 namespace {
 
 
-// A device buffer from the runner stream's pool; freed (stream-ordered) on scope exit.
+// Caching device allocator, one free list per stream. All work that touches a
+// block is enqueued on the stream it was taken for, so a block returned to the
+// list can be handed out again at once: any later use is ordered after every
+// earlier one on that stream. Blocks go back to the device only when the
+// stream's runner is destroyed.
+class StreamPool {
+  public:
+    static StreamPool &instance() {
+        static StreamPool pool;
+        return pool;
+    }
+    void *take(hipStream_t s, size_t bytes) {
+        bytes = round_up(bytes);
+        {
+            std::lock_guard<std::mutex> lock(mu_);
+            auto &free = free_[s];
+            auto it = free.lower_bound(bytes);
+            if (it != free.end() && it->first <= 2 * bytes + (2u << 20)) {
+                void *p = it->second;
+                sizes_[p] = it->first;
+                free.erase(it);
+                return p;
+            }
+        }
+        void *p = nullptr;
+        hipError_t e = hipMalloc(&p, bytes);
+        if (e != hipSuccess) {
+            // Release this stream's cached blocks and try once more.
+            trim(s);
+            DMX_HIP(hipMalloc(&p, bytes));
+        }
+        std::lock_guard<std::mutex> lock(mu_);
+        sizes_[p] = bytes;
+        owner_[p] = s;
+        return p;
+    }
+    void give(hipStream_t s, void *p) {
+        std::lock_guard<std::mutex> lock(mu_);
+        auto it = sizes_.find(p);
+        if (it == sizes_.end()) return;
+        free_[s].emplace(it->second, p);
+        sizes_.erase(it);
+    }
+    // Frees every cached block of `s` (after the stream has drained).
+    void trim(hipStream_t s) {
+        (void)hipStreamSynchronize(s);
+        std::lock_guard<std::mutex> lock(mu_);
+        auto &free = free_[s];
+        for (auto &kv : free) {
+            (void)hipFree(kv.second);
+            owner_.erase(kv.second);
+        }
+        free.clear();
+    }
+
+  private:
+    static size_t round_up(size_t b) {
+        const size_t g = b >= (1u << 20) ? (1u << 20) : 512;
+        return (std::max<size_t>(b, 1) + g - 1) / g * g;
+    }
+    std::mutex mu_;
+    std::map<hipStream_t, std::multimap<size_t, void *>> free_;
+    std::map<void *, size_t> sizes_;     // blocks in use -> size
+    std::map<void *, hipStream_t> owner_;
+};
+
+// A device buffer from the stream's cache, returned to it on scope exit.
 struct DBuf {
     hipStream_t s = nullptr;
     void *p = nullptr;
     size_t bytes = 0;
     DBuf() = default;
     DBuf(hipStream_t stream, size_t n_bytes) : s(stream), bytes(n_bytes) {
-        if (bytes) DMX_HIP(hipMallocAsync(&p, bytes, s));
+        if (bytes) p = StreamPool::instance().take(s, bytes);
     }
     DBuf(const DBuf &) = delete;
     DBuf &operator=(const DBuf &) = delete;
@@ -51,7 +117,7 @@ struct DBuf {
     }
     ~DBuf() { release(); }
     void release() {
-        if (p) (void)hipFreeAsync(p, s);
+        if (p) StreamPool::instance().give(s, p);
         p = nullptr;
     }
     float *f() const { return static_cast<float *>(p); }
@@ -977,11 +1043,6 @@ int dmx_runner_create(const dmx_tensor *weights, size_t n_weights, const dmx_con
         DMX_HIP(hipGetDeviceProperties(&prop, device_ordinal));
         r->tag = std::string("hip:") + prop.name + ":" + prop.gcnArchName;
         DMX_HIP(hipStreamCreateWithFlags(&r->stream, hipStreamNonBlocking));
-        hipMemPool_t pool;
-        if (hipDeviceGetDefaultMemPool(&pool, device_ordinal) == hipSuccess) {
-            uint64_t threshold = UINT64_MAX;
-            (void)hipMemPoolSetAttribute(pool, hipMemPoolAttrReleaseThreshold, &threshold);
-        }
         load_weights(*r, weights, n_weights);
     });
     if (rc != DMX_OK) {
@@ -997,7 +1058,10 @@ int dmx_runner_create(const dmx_tensor *weights, size_t n_weights, const dmx_con
 void dmx_runner_destroy(dmx_runner *r) {
     if (!r) return;
     (void)hipSetDevice(r->device);
-    if (r->stream) (void)hipStreamSynchronize(r->stream);
+    if (r->stream) {
+        (void)hipStreamSynchronize(r->stream);
+        StreamPool::instance().trim(r->stream);
+    }
     if (r->weight_mem) (void)hipFree(r->weight_mem);
     for (void *p : r->owned) (void)hipFree(p);
     if (r->stream) (void)hipStreamDestroy(r->stream);

@@ -148,7 +148,8 @@ def test_conv_transpose_matches_oracle(lib, oracle, b, ic, A, P, oc, last):
     assert rms_relative_error(ref, out.cpu().numpy()) < 1e-5
 
 
-@pytest.mark.parametrize("B,C,F,T", [(1, 48, 16, 40), (2, 96, 1, 700), (1, 384, 2, 33)])
+@pytest.mark.parametrize("B,C,F,T", [(1, 48, 16, 40), (2, 96, 1, 700), (1, 384, 2, 33), (2, 192, 3, 300),
+                                     (1, 48, 1, 1000)])
 def test_dconv_matches_oracle(lib, oracle, dmx, B, C, F, T):
     r = rng(C + T)
     hid = C // 8

@@ -1,0 +1,69 @@
+"""Chunking / overlap-add / shift / bag invariants of the oracle's separation
+loop, with stand-in forwards (the reference's `IdForward` pattern,
+crates/demucs-core/src/demucs/streaming.rs:657-926, core/tests/streaming_ola.rs:109-233).
+"""
+import numpy as np
+import pytest
+
+from conftest import snr_db
+
+
+def identity_forward(chunk):
+    """Every source gets the chunk itself: the OLA must give the mix back."""
+    return np.repeat(chunk[:, None], 4, axis=1)
+
+
+def scaled_forward(chunk):
+    """Source s gets (s + 1) * chunk (a linear, source-dependent stand-in)."""
+    return np.stack([chunk * (s + 1) for s in range(4)], axis=1)
+
+
+@pytest.mark.parametrize("length,seg,group", [(1000, 160, 1), (1000, 160, 3), (159, 160, 1), (161, 160, 2),
+                                              (4000, 1000, 8)])
+def test_identity_forward_reconstructs_the_normalised_mix(oracle, length, seg, group):
+    mix = np.random.default_rng(length).normal(size=(1, 2, length)).astype(np.float32)
+    out = oracle.split_pass(mix, seg, 0.25, 1.0, 0, 0, group, 4, identity_forward)
+    for s in range(4):
+        np.testing.assert_allclose(out[0, s], mix[0], rtol=1e-5, atol=1e-6)
+
+
+def test_grouping_is_a_scheduling_change_only(oracle):  # pipeline.rs:774-839
+    mix = np.random.default_rng(1).normal(size=(1, 2, 2500)).astype(np.float32)
+    one = oracle.split_pass(mix, 400, 0.25, 1.0, 0, 0, 1, 4, scaled_forward)
+    three = oracle.split_pass(mix, 400, 0.25, 1.0, 0, 0, 3, 4, scaled_forward)
+    np.testing.assert_array_equal(one, three)
+
+
+def test_chunk_count_is_ceil_length_over_stride(oracle):  # streaming.rs:87-94
+    calls = []
+    mix = np.zeros((1, 2, 687960), np.float32)
+    oracle.split_pass(mix, 343980, 0.25, 1.0, 0, 0, 1, 4, lambda c: calls.append(1) or identity_forward(c))
+    assert len(calls) == 3  # num_chunks_for(687960, 343980, 257985) == 3
+
+
+@pytest.mark.parametrize("shifts", [0, 1, 2])
+def test_separate_with_identity_forward_returns_the_mix(dmx, oracle, shifts):
+    """Global normalisation, chunking, OLA, shift view + trim and the final
+    denormalisation compose to the identity."""
+    rng = np.random.default_rng(shifts)
+    left, right = (rng.normal(size=30000) * 0.3).astype(np.float32), (rng.normal(size=30000) * 0.3).astype(np.float32)
+    opts = dmx.SeparateOptions(shifts=shifts, overlap=0.25, segment=4410 / 44100, batch_chunks=2)
+    out = oracle.separate([], left, right, 44100, opts, forward=identity_forward)
+    for s in range(4):
+        assert snr_db(left, out[s, 0]) > 110 and snr_db(right, out[s, 1]) > 110
+
+
+def test_a_linear_forward_commutes_with_the_overlap_add(dmx, oracle):
+    """Scaling a source inside the forward scales the normalised stem: the OLA,
+    trim and denormalisation are linear in the forward's output."""
+    rng = np.random.default_rng(3)
+    left, right = rng.normal(size=9000).astype(np.float32), rng.normal(size=9000).astype(np.float32)
+    opts = dmx.SeparateOptions(shifts=0, segment=2205 / 44100)
+    single = oracle.separate([], left, right, 44100, opts, forward=scaled_forward)
+    ident = oracle.separate([], left, right, 44100, opts, forward=identity_forward)
+    # stem s of the scaled forward is (s + 1) times the identity's, minus the
+    # (s + 1 - 1) * mean offset the denormalisation adds once.
+    m, sd = oracle.scan_norm(np.stack([left, right])[None])
+    for s in range(4):
+        expect = (ident[s] - m) * (s + 1) + m
+        assert snr_db(expect, single[s]) > 100
