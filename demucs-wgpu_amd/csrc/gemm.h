@@ -30,12 +30,21 @@ namespace dmx {
 
 typedef float floatx16 __attribute__((ext_vector_type(16)));
 
-constexpr int GEMM_BK = 16;
+// k-tile depth. 16 measured faster than 32 at every model shape on MI355X:
+// the double-buffered 128x128x16 stage (33 KB of LDS) keeps three workgroups
+// per CU resident, and occupancy hides the global-load latency better than a
+// deeper stage does.
+#ifndef DMX_GEMM_BK
+#define DMX_GEMM_BK 16
+#endif
+constexpr int GEMM_BK = DMX_GEMM_BK;
 constexpr int GEMM_THREADS = 256;
 
 template <int BM, int BN, int WAVES_M, bool GLU, class AL, class BL, class EP>
 __global__ __launch_bounds__(GEMM_THREADS) void gemm_kernel(int M, int N, int K, AL al, BL bl, EP ep) {
     constexpr int BK = GEMM_BK;
+    constexpr int KQ = BK / 4;  // float4 chunks per k-major row of a stage
+    static_assert(BK % 4 == 0, "BK must be a multiple of 4");
     constexpr int WAVES_N = 4 / WAVES_M;
     constexpr int WTM = BM / WAVES_M, WTN = BN / WAVES_N;
     constexpr int TM = WTM / 32, TN = WTN / 32;
@@ -84,7 +93,7 @@ __global__ __launch_bounds__(GEMM_THREADS) void gemm_kernel(int M, int N, int K,
 #pragma unroll
     for (int it = 0; it < A_STATES; ++it) {
         int e = tid + it * GEMM_THREADS;
-        int lr = AL::kmajor ? e / 4 : e % BM;
+        int lr = AL::kmajor ? e / KQ : e % BM;
         bool in_tile = AL::kmajor ? (e < BM * BK / 4) : (e < BM * BK);
         int pr = in_tile ? phys_row(lr) : -1;
         aok[it] = pr >= 0;
@@ -93,7 +102,7 @@ __global__ __launch_bounds__(GEMM_THREADS) void gemm_kernel(int M, int N, int K,
 #pragma unroll
     for (int it = 0; it < B_STATES; ++it) {
         int e = tid + it * GEMM_THREADS;
-        int lc = BL::kmajor ? e / 4 : e % BN;
+        int lc = BL::kmajor ? e / KQ : e % BN;
         bool in_tile = BL::kmajor ? (e < BN * BK / 4) : (e < BN * BK);
         int n = n0 + lc;
         bok[it] = in_tile && n < N;
@@ -107,7 +116,7 @@ __global__ __launch_bounds__(GEMM_THREADS) void gemm_kernel(int M, int N, int K,
         for (int it = 0; it < A_STATES; ++it) {
             int e = tid + it * GEMM_THREADS;
             if constexpr (AL::kmajor) {
-                int k = k0 + 4 * (e % 4);
+                int k = k0 + 4 * (e % KQ);
                 float4 v = aok[it] ? al.load4(ast[it], k, K) : make_float4(0.f, 0.f, 0.f, 0.f);
                 areg[4 * it + 0] = v.x;
                 areg[4 * it + 1] = v.y;
@@ -122,7 +131,7 @@ __global__ __launch_bounds__(GEMM_THREADS) void gemm_kernel(int M, int N, int K,
         for (int it = 0; it < B_STATES; ++it) {
             int e = tid + it * GEMM_THREADS;
             if constexpr (BL::kmajor) {
-                int k = k0 + 4 * (e % 4);
+                int k = k0 + 4 * (e % KQ);
                 float4 v = bok[it] ? bl.load4(bst[it], k, K) : make_float4(0.f, 0.f, 0.f, 0.f);
                 breg[4 * it + 0] = v.x;
                 breg[4 * it + 1] = v.y;
@@ -141,7 +150,7 @@ __global__ __launch_bounds__(GEMM_THREADS) void gemm_kernel(int M, int N, int K,
             int e = tid + it * GEMM_THREADS;
             if constexpr (AL::kmajor) {
                 if (e < BM * BK / 4) {
-                    int lr = e / 4, kk = 4 * (e % 4);
+                    int lr = e / KQ, kk = 4 * (e % KQ);
 #pragma unroll
                     for (int j = 0; j < 4; ++j) As[buf][kk + j][lr] = areg[4 * it + j];
                 }
@@ -154,7 +163,7 @@ __global__ __launch_bounds__(GEMM_THREADS) void gemm_kernel(int M, int N, int K,
             int e = tid + it * GEMM_THREADS;
             if constexpr (BL::kmajor) {
                 if (e < BN * BK / 4) {
-                    int lc = e / 4, kk = 4 * (e % 4);
+                    int lc = e / KQ, kk = 4 * (e % KQ);
 #pragma unroll
                     for (int j = 0; j < 4; ++j) Bs[buf][kk + j][lc] = breg[4 * it + j];
                 }
