@@ -75,6 +75,33 @@ def attention_roofline(pkg, torch, batch: int, iters: int):
     return ms, flops
 
 
+TRAFFIC_SUMMARY = ROOT / "profiles" / "attention_cross_b8_traffic.md"
+
+
+def measured_traffic():
+    """HBM bytes per launch of the roofline kernel, from the committed
+    rocprofv3 FETCH_SIZE / WRITE_SIZE summary (copy-kernel calibrated), or None."""
+    try:
+        for line in TRAFFIC_SUMMARY.read_text().splitlines():
+            if line.startswith("traffic_bytes_per_launch:"):
+                return int(line.split(":", 1)[1].strip())
+    except OSError:
+        pass
+    return None
+
+
+def copy_calibration(torch, mib: int = 256, iters: int = 5):
+    """A plain device copy of known size: rocprofv3's FETCH_SIZE / WRITE_SIZE for
+    this kernel over `mib` MiB read and written gives the counters' scale."""
+    n = mib * (1 << 20) // 4
+    src = torch.ones(n, device="cuda")
+    dst = torch.empty(n, device="cuda")
+    for _ in range(iters):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    return mib
+
+
 def cpu_baseline(pkg, seconds_budget: float = 20.0):
     """The restated reference CPU backend on one 7.8 s segment (config 1):
     1 warm-up, then the median of up to 3 timed forwards within the budget."""
@@ -108,6 +135,8 @@ def main():
     ap.add_argument("--batch-chunks", type=int, default=8)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--attn-iters", type=int, default=20)
+    ap.add_argument("--roofline-only", action="store_true",
+                    help="only the roofline kernel loop and the copy calibration (for rocprofv3 runs)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py: this build runs on one GPU only; multi-GPU runs are not part of it "
@@ -116,6 +145,13 @@ def main():
 
     import torch
     pkg = load_package()
+    if args.roofline_only:
+        attn_ms, attn_flops = attention_roofline(pkg, torch, args.batch_chunks, args.attn_iters)
+        mib = copy_calibration(torch)
+        print(json.dumps({"kernel": "attention_kernel", "avg_ms": round(attn_ms, 4),
+                          "tflops": round(attn_flops / (attn_ms * 1e-3) / 1e12, 2),
+                          "flops_per_launch": attn_flops, "copy_calibration_mib": mib}))
+        return
     cfg = pkg.Config()
     weights = pkg.random_init(0, cfg)
     runner = pkg.Runner(weights, cfg, device=0)
@@ -153,7 +189,7 @@ def main():
     attn_ms, attn_flops = attention_roofline(pkg, torch, args.batch_chunks, args.attn_iters)
     attn_tflops = attn_flops / (attn_ms * 1e-3) / 1e12
     roofline = {"bound": "mfma", "achieved": round(attn_tflops, 2), "peak": FP32_MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
-                "frac": round(attn_tflops / FP32_MFMA_PEAK_TFLOPS, 4), "traffic": None,
+                "frac": round(attn_tflops / FP32_MFMA_PEAK_TFLOPS, 4), "traffic": measured_traffic(),
                 "kernel": "attention_kernel (fused cross-attention, fp32 MFMA)",
                 "per_launch": f"4*B*Lq*Lk*512 flops, B={args.batch_chunks}, (Lq, Lk) = (2688, 1344) and (1344, 2688); "
                               f"avg {attn_ms:.3f} ms per launch"}

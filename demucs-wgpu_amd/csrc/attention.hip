@@ -3,13 +3,14 @@
 //
 // Semantics: `attention_head` (crates/demucs-core/src/demucs/ops.rs:1350-1408):
 // scaled = q * scale; S = scaled k^T; P = exp(S - rowmax); O = P v / rowsum.
-// Here the row max is the running max over key tiles (online softmax), so the
+// Here the row max is a running max over key tiles (online softmax), so the
 // Lq x Lk score matrix (231 MB per (b, h) for 2688^2 on the reference device)
 // never exists; results agree to f32 rounding.
 //
 // CDNA4 layout. A workgroup = 4 waves = 128 queries of one (batch, head); each
-// wave owns 32 queries. Keys stream through LDS in tiles of 64 (K and V,
-// prefetched into registers during the previous tile's math).
+// wave owns 32 queries. Keys stream through LDS in tiles of 64, double
+// buffered: the next tile is fetched into registers while the current one is
+// multiplied, then written to the other buffer, so one barrier per tile.
 //   * Scores are computed transposed, S^T = K Q^T, with v_mfma_f32_32x32x2f32:
 //     lane l then holds query l%32 for 32 keys in registers, so row max / row
 //     sum need only in-lane reductions plus one cross-half shuffle.
@@ -18,8 +19,24 @@
 //     never leaves registers.
 //   * The d contraction of QK^T pairs dim s with lane half 0 and dim 32+s with
 //     lane half 1, so each lane's Q fragment is one contiguous 32-float run.
+//   * K is kept [key][d] and V transposed [d][key] in LDS, rows padded to 68
+//     floats: every MFMA operand then comes from a 128-bit LDS read (4 MFMAs
+//     per read), and the reads and the staging writes are bank-conflict free.
+//   * Scores live in log2 units (Q is pre-scaled by scale * log2 e), so each
+//     probability is one v_exp_f32. The running max is raised lazily: only
+//     when some query's tile max exceeds it by more than ATT_SLACK, so the
+//     accumulator rescale is skipped on most tiles while exp2(s - m) stays
+//     below 2^ATT_SLACK. O and the row sum carry the same factor, which the
+//     final division cancels.
+#include <type_traits>
+
 #include "common.h"
 #include "ops.h"
+
+// Waves per SIMD the register allocation must leave room for.
+#ifndef DMX_ATT_WAVES_PER_EU
+#define DMX_ATT_WAVES_PER_EU 2
+#endif
 
 namespace dmx {
 namespace {
@@ -30,15 +47,18 @@ constexpr int ATT_D = 64;
 constexpr int ATT_KT = 64;      // keys per tile
 constexpr int ATT_QW = 32;      // queries per wave
 constexpr int ATT_WAVES = 4;
-constexpr int ATT_LD = ATT_D + 1;
+constexpr int ATT_LD = 68;      // padded LDS row (floats); 16-byte aligned rows
+constexpr float ATT_LOG2E = 1.4426950408889634f;
+constexpr float ATT_SLACK = 8.0f;
 
-__global__ __launch_bounds__(256) void attention_kernel(const float *__restrict__ q, int64_t ldq,
-                                                        const float *__restrict__ k, int64_t ldk,
-                                                        const float *__restrict__ v, int64_t ldv,
-                                                        float *__restrict__ out, int64_t ldo, int n_q, int n_k,
-                                                        float scale, int64_t q_bs, int64_t kv_bs, int64_t o_bs) {
-    __shared__ float Ks[ATT_KT][ATT_LD];
-    __shared__ float Vs[ATT_KT][ATT_LD];
+__device__ __forceinline__ float4 lds4(const float *p) { return *reinterpret_cast<const float4 *>(p); }
+
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(DMX_ATT_WAVES_PER_EU)))
+void attention_kernel(const float *__restrict__ q, int64_t ldq, const float *__restrict__ k, int64_t ldk,
+                      const float *__restrict__ v, int64_t ldv, float *__restrict__ out, int64_t ldo, int n_q,
+                      int n_k, float scale, int64_t q_bs, int64_t kv_bs, int64_t o_bs) {
+    __shared__ __align__(16) float Ks[2][ATT_KT][ATT_LD];  // [buffer][key][d]
+    __shared__ __align__(16) float Vt[2][ATT_D][ATT_LD];   // [buffer][d][key]
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int head = blockIdx.y, b = blockIdx.z;
@@ -50,124 +70,149 @@ __global__ __launch_bounds__(256) void attention_kernel(const float *__restrict_
     const float *kb = k + b * kv_bs + head * ATT_D;
     const float *vb = v + b * kv_bs + head * ATT_D;
 
-    // Q fragment: dims [32*half, 32*half + 32) of this lane's query, pre-scaled.
+    // Q fragment: dims [32*half, 32*half + 32) of this lane's query, pre-scaled
+    // into log2 units.
     float qreg[32];
     {
+        const float qs = scale * ATT_LOG2E;
         const float *row = qb + (int64_t)(q_ok ? qi : 0) * ldq + 32 * half;
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
             float4 t = q_ok ? *reinterpret_cast<const float4 *>(row + 4 * i) : make_float4(0.f, 0.f, 0.f, 0.f);
-            qreg[4 * i + 0] = t.x * scale;
-            qreg[4 * i + 1] = t.y * scale;
-            qreg[4 * i + 2] = t.z * scale;
-            qreg[4 * i + 3] = t.w * scale;
+            qreg[4 * i + 0] = t.x * qs;
+            qreg[4 * i + 1] = t.y * qs;
+            qreg[4 * i + 2] = t.z * qs;
+            qreg[4 * i + 3] = t.w * qs;
         }
     }
 
-    // K/V tile staging: 64 keys x 64 dims each = 1024 float4 per tensor, 4 per thread.
+    // Tile staging: 64 keys x 16 float4 per tensor; slot i of this thread is
+    // key 16*(s%4) + lane%16, float4 column 4*(s/4) + lane/16 with s = 4*wave + i.
+    // A wave then writes 16 keys x 4 columns at once, which keeps the
+    // transposed V writes on 64 distinct banks.
     float4 kpre[4], vpre[4];
+    auto slot_key = [&](int i) { return 16 * ((4 * wave + i) & 3) + (lane & 15); };
+    auto slot_d4 = [&](int i) { return 4 * ((4 * wave + i) >> 2) + (lane >> 4); };
     auto fetch = [&](int key0) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            int e = tid + 256 * i, key = e >> 4, d4 = e & 15;
-            int kk = key0 + key;
+            const int kk = key0 + slot_key(i), d = 4 * slot_d4(i);
             if (kk < n_k) {
-                kpre[i] = *reinterpret_cast<const float4 *>(kb + (int64_t)kk * ldk + 4 * d4);
-                vpre[i] = *reinterpret_cast<const float4 *>(vb + (int64_t)kk * ldv + 4 * d4);
+                kpre[i] = *reinterpret_cast<const float4 *>(kb + (int64_t)kk * ldk + d);
+                vpre[i] = *reinterpret_cast<const float4 *>(vb + (int64_t)kk * ldv + d);
             } else {
                 kpre[i] = make_float4(0.f, 0.f, 0.f, 0.f);
                 vpre[i] = make_float4(0.f, 0.f, 0.f, 0.f);
             }
         }
     };
-    auto stage = [&]() {
+    auto stage = [&](int buf) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            int e = tid + 256 * i, key = e >> 4, d = 4 * (e & 15);
-            Ks[key][d + 0] = kpre[i].x;
-            Ks[key][d + 1] = kpre[i].y;
-            Ks[key][d + 2] = kpre[i].z;
-            Ks[key][d + 3] = kpre[i].w;
-            Vs[key][d + 0] = vpre[i].x;
-            Vs[key][d + 1] = vpre[i].y;
-            Vs[key][d + 2] = vpre[i].z;
-            Vs[key][d + 3] = vpre[i].w;
+            const int key = slot_key(i), d = 4 * slot_d4(i);
+            *reinterpret_cast<float4 *>(&Ks[buf][key][d]) = kpre[i];
+            Vt[buf][d + 0][key] = vpre[i].x;
+            Vt[buf][d + 1][key] = vpre[i].y;
+            Vt[buf][d + 2][key] = vpre[i].z;
+            Vt[buf][d + 3][key] = vpre[i].w;
         }
     };
 
-    floatx16 o0, o1;
-#pragma unroll
-    for (int r = 0; r < 16; ++r) {
-        o0[r] = 0.0f;
-        o1[r] = 0.0f;
-    }
+    const floatx16 zero = {};
+    floatx16 o0 = zero, o1 = zero;
     float m_run = -INFINITY, l_run = 0.0f;
 
-    const int tiles = (n_k + ATT_KT - 1) / ATT_KT;
-    fetch(0);
-    stage();
-    __syncthreads();
-    for (int t = 0; t < tiles; ++t) {
-        const int key0 = t * ATT_KT;
-        if (t + 1 < tiles) fetch(key0 + ATT_KT);
-
-        // S^T for keys [key0, key0+32) and [key0+32, key0+64).
+    // One 64-key tile; MASK only for a ragged last tile.
+    auto tile = [&](auto mask_tag, int buf, int key0) {
+        constexpr bool MASK = decltype(mask_tag)::value;
+        // S^T for keys [key0, key0+32) (s0) and [key0+32, key0+64) (s1).
         floatx16 s0, s1;
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-            s0[r] = 0.0f;
-            s1[r] = 0.0f;
-        }
+        for (int c = 0; c < 8; ++c) {
+            const float4 ka = lds4(&Ks[buf][j][32 * half + 4 * c]);
+            const float4 kc = lds4(&Ks[buf][32 + j][32 * half + 4 * c]);
+            const float av[4] = {ka.x, ka.y, ka.z, ka.w};
+            const float cv[4] = {kc.x, kc.y, kc.z, kc.w};
 #pragma unroll
-        for (int s = 0; s < 32; ++s) {
-            float a0 = Ks[j][32 * half + s];
-            float a1 = Ks[32 + j][32 * half + s];
-            s0 = __builtin_amdgcn_mfma_f32_32x32x2f32(a0, qreg[s], s0, 0, 0, 0);
-            s1 = __builtin_amdgcn_mfma_f32_32x32x2f32(a1, qreg[s], s1, 0, 0, 0);
+            for (int e = 0; e < 4; ++e) {
+                const int s = 4 * c + e;
+                s0 = __builtin_amdgcn_mfma_f32_32x32x2f32(av[e], qreg[s], s == 0 ? zero : s0, 0, 0, 0);
+                s1 = __builtin_amdgcn_mfma_f32_32x32x2f32(cv[e], qreg[s], s == 0 ? zero : s1, 0, 0, 0);
+            }
         }
-        // Register r of lane l holds key key0 + tile*32 + 8*(r/4) + 4*half + r%4.
-        float mloc = -INFINITY;
+        // Register r of lane l holds key key0 + 8*(r/4) + 4*half + r%4 (s0), +32 (s1).
+        if constexpr (MASK) {
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-            int kk = key0 + 8 * (r >> 2) + 4 * half + (r & 3);
-            if (kk >= n_k) s0[r] = -INFINITY;
-            if (kk + 32 >= n_k) s1[r] = -INFINITY;
-            mloc = fmaxf(mloc, fmaxf(s0[r], s1[r]));
+            for (int r = 0; r < 16; ++r) {
+                const int kk = key0 + 8 * (r >> 2) + 4 * half + (r & 3);
+                if (kk >= n_k) s0[r] = -INFINITY;
+                if (kk + 32 >= n_k) s1[r] = -INFINITY;
+            }
         }
+        float mloc = fmaxf(s0[0], s1[0]);
+#pragma unroll
+        for (int r = 1; r < 16; ++r) mloc = fmaxf(mloc, fmaxf(s0[r], s1[r]));
         mloc = fmaxf(mloc, __shfl_xor(mloc, 32, 64));
-        const float m_new = fmaxf(m_run, mloc);
-        const float corr = expf(m_run - m_new);
+        if (__any(mloc > m_run + ATT_SLACK)) {  // uniform branch; always taken on the first tile
+            const float m_new = fmaxf(m_run, mloc);
+            const float corr = __builtin_amdgcn_exp2f(m_run - m_new);
+            l_run *= corr;
+            m_run = m_new;
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                o0[r] *= corr;
+                o1[r] *= corr;
+            }
+        }
         float lsum = 0.0f;
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
-            s0[r] = expf(s0[r] - m_new);
-            s1[r] = expf(s1[r] - m_new);
+            s0[r] = __builtin_amdgcn_exp2f(s0[r] - m_run);
+            s1[r] = __builtin_amdgcn_exp2f(s1[r] - m_run);
             lsum += s0[r] + s1[r];
         }
         lsum += __shfl_xor(lsum, 32, 64);
-        l_run = l_run * corr + lsum;
-        m_run = m_new;
+        l_run += lsum;
+        // O^T += V^T P^T, contracting keys in the order the score registers
+        // hold them: registers 4a..4a+3 are keys 8a + 4*half + 0..3.
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-            o0[r] *= corr;
-            o1[r] *= corr;
-        }
-        // O^T += V^T P^T, contracting keys in the order the score registers hold them.
+        for (int a = 0; a < 4; ++a) {
+            const float4 v0 = lds4(&Vt[buf][j][8 * a + 4 * half]);
+            const float4 v1 = lds4(&Vt[buf][32 + j][8 * a + 4 * half]);
+            const float4 w0 = lds4(&Vt[buf][j][32 + 8 * a + 4 * half]);
+            const float4 w1 = lds4(&Vt[buf][32 + j][32 + 8 * a + 4 * half]);
+            const float v0v[4] = {v0.x, v0.y, v0.z, v0.w}, v1v[4] = {v1.x, v1.y, v1.z, v1.w};
+            const float w0v[4] = {w0.x, w0.y, w0.z, w0.w}, w1v[4] = {w1.x, w1.y, w1.z, w1.w};
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-            const int kr = 8 * (r >> 2) + 4 * half + (r & 3);
-            o0 = __builtin_amdgcn_mfma_f32_32x32x2f32(Vs[kr][j], s0[r], o0, 0, 0, 0);
-            o1 = __builtin_amdgcn_mfma_f32_32x32x2f32(Vs[kr][32 + j], s0[r], o1, 0, 0, 0);
-        }
+            for (int e = 0; e < 4; ++e) {
+                o0 = __builtin_amdgcn_mfma_f32_32x32x2f32(v0v[e], s0[4 * a + e], o0, 0, 0, 0);
+                o1 = __builtin_amdgcn_mfma_f32_32x32x2f32(v1v[e], s0[4 * a + e], o1, 0, 0, 0);
+            }
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-            const int kr = 32 + 8 * (r >> 2) + 4 * half + (r & 3);
-            o0 = __builtin_amdgcn_mfma_f32_32x32x2f32(Vs[kr][j], s1[r], o0, 0, 0, 0);
-            o1 = __builtin_amdgcn_mfma_f32_32x32x2f32(Vs[kr][32 + j], s1[r], o1, 0, 0, 0);
+            for (int e = 0; e < 4; ++e) {
+                o0 = __builtin_amdgcn_mfma_f32_32x32x2f32(w0v[e], s1[4 * a + e], o0, 0, 0, 0);
+                o1 = __builtin_amdgcn_mfma_f32_32x32x2f32(w1v[e], s1[4 * a + e], o1, 0, 0, 0);
+            }
         }
-        __syncthreads();
-        if (t + 1 < tiles) {
-            stage();
+    };
+
+    const int tiles = (n_k + ATT_KT - 1) / ATT_KT;
+    const bool ragged = (n_k % ATT_KT) != 0;
+    fetch(0);
+    stage(0);
+    __syncthreads();
+    for (int t = 0; t < tiles; ++t) {
+        const int buf = t & 1;
+        const bool more = t + 1 < tiles;
+        if (more) fetch((t + 1) * ATT_KT);
+        if (!more && ragged)
+            tile(std::true_type{}, buf, t * ATT_KT);
+        else
+            tile(std::false_type{}, buf, t * ATT_KT);
+        if (more) {
+            // The other buffer was last read in tile t-1, which every wave
+            // finished before the previous barrier.
+            stage(buf ^ 1);
             __syncthreads();
         }
     }

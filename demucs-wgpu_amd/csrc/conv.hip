@@ -276,6 +276,11 @@ void gemm_auto(hipStream_t s, int M, int N, int K, int batches, const AL &al, co
         else
             launch_gemm<64, 128, 1, true>(s, M, N, K, batches, al, bl, ep);
     } else {
+#ifdef DMX_BIG_BM  // tuning builds only: a larger tile for tall problems
+        if (M >= DMX_BIG_BM)
+            launch_gemm<DMX_BIG_BM, DMX_BIG_BN, DMX_BIG_WM, false>(s, M, N, K, batches, al, bl, ep);
+        else
+#endif
         if (M >= 96)
             launch_gemm<128, 128, 2, false>(s, M, N, K, batches, al, bl, ep);
         else if (M > 32)

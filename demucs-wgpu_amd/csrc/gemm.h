@@ -16,24 +16,30 @@
 // (BN/WAVES_N) sub-tile computed as 32x32 tiles with v_mfma_f32_32x32x2f32
 // (A: lane l holds A[l%32][l/32]; B: lane l holds B[l/32][l%32];
 // D: 16 regs, reg r of lane l is D[8*(r/4) + 4*(l/32) + r%4][l%32]).
-// Operand tiles go global -> registers -> LDS (double buffered, one barrier
-// per BK step), so the next tile's global loads overlap this tile's MFMAs.
+// Both operand tiles sit in LDS k-contiguous, [row][k], rows padded to BK + 4
+// floats so that 16 consecutive rows start on distinct bank quads. The k
+// contraction is reordered in groups of 8: at MFMA step t lane half h
+// contributes k = 8g + 4h + t, so one ds_read_b128 of row[8g + 4h .. +3]
+// feeds four MFMAs. Tiles go global -> registers -> LDS (double buffered, one
+// barrier per BK step), so the next tile's global loads overlap this tile's
+// MFMAs. k-major sources are read as float4 along k; m/n-major sources are
+// read four k at a time per column (coalesced across lanes along m/n).
 //
 // GLU mode: each wave's two 32-row m-tiles hold the value channels c and the
 // gate channels C + c of the same outputs, so GLU happens in registers and the
 // 2C-channel product is never written.
 #pragma once
 
+#include <type_traits>
+
 #include "common.h"
 
 namespace dmx {
 
 typedef float floatx16 __attribute__((ext_vector_type(16)));
+typedef float floatx4 __attribute__((ext_vector_type(4)));
 
-// k-tile depth. 16 measured faster than 32 at every model shape on MI355X:
-// the double-buffered 128x128x16 stage (33 KB of LDS) keeps three workgroups
-// per CU resident, and occupancy hides the global-load latency better than a
-// deeper stage does.
+// k-tile depth.
 #ifndef DMX_GEMM_BK
 #define DMX_GEMM_BK 16
 #endif
@@ -43,16 +49,16 @@ constexpr int GEMM_THREADS = 256;
 template <int BM, int BN, int WAVES_M, bool GLU, class AL, class BL, class EP>
 __global__ __launch_bounds__(GEMM_THREADS) void gemm_kernel(int M, int N, int K, AL al, BL bl, EP ep) {
     constexpr int BK = GEMM_BK;
-    constexpr int KQ = BK / 4;  // float4 chunks per k-major row of a stage
-    static_assert(BK % 4 == 0, "BK must be a multiple of 4");
+    constexpr int KQ = BK / 4;   // float4 chunks per row of a stage
+    constexpr int LD = BK + 4;   // LDS row stride (floats)
+    static_assert(BK % 8 == 0, "BK must be a multiple of 8");
     constexpr int WAVES_N = 4 / WAVES_M;
     constexpr int WTM = BM / WAVES_M, WTN = BN / WAVES_N;
     constexpr int TM = WTM / 32, TN = WTN / 32;
     static_assert(TM >= 1 && TN >= 1, "wave tile must hold at least one 32x32 MFMA tile");
     static_assert(!GLU || TM == 2, "GLU needs exactly one value and one gate tile per wave");
-    constexpr int LDA = BM + 2, LDB = BN + 2;  // row stride = 2 mod 32 banks
-    __shared__ float As[2][BK][LDA];
-    __shared__ float Bs[2][BK][LDB];
+    __shared__ __align__(16) float As[2][BM][LD];
+    __shared__ __align__(16) float Bs[2][BN][LD];
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int wm = wave % WAVES_M, wn = wave / WAVES_M;
@@ -74,102 +80,66 @@ __global__ __launch_bounds__(GEMM_THREADS) void gemm_kernel(int M, int N, int K,
         }
     };
 
-    // ---- A operand staging ----
-    // k-major sources: 4 consecutive k per thread (a float4 when aligned).
-    // m-major sources: one element per thread per pass, consecutive threads on
-    // consecutive rows.
-    constexpr int A_KM_ITEMS = (BM * BK / 4 + GEMM_THREADS - 1) / GEMM_THREADS;
-    constexpr int A_MM_ITEMS = (BM * BK + GEMM_THREADS - 1) / GEMM_THREADS;
-    constexpr int B_KM_ITEMS = (BN * BK / 4 + GEMM_THREADS - 1) / GEMM_THREADS;
-    constexpr int B_MM_ITEMS = (BN * BK + GEMM_THREADS - 1) / GEMM_THREADS;
-    constexpr int A_REGS = AL::kmajor ? A_KM_ITEMS * 4 : A_MM_ITEMS;
-    constexpr int B_REGS = BL::kmajor ? B_KM_ITEMS * 4 : B_MM_ITEMS;
-    constexpr int A_STATES = AL::kmajor ? A_KM_ITEMS : A_MM_ITEMS;
-    constexpr int B_STATES = BL::kmajor ? B_KM_ITEMS : B_MM_ITEMS;
+    // ---- operand staging: items are (row, k-quad) pairs, one float4 each ----
+    // k-major: item e = (row e / KQ, quad e % KQ); m/n-major: (row e % R, quad e / R).
+    constexpr int A_ITEMS = (BM * KQ + GEMM_THREADS - 1) / GEMM_THREADS;
+    constexpr int B_ITEMS = (BN * KQ + GEMM_THREADS - 1) / GEMM_THREADS;
+    auto a_row = [&](int e) { return AL::kmajor ? e / KQ : e % BM; };
+    auto a_quad = [&](int e) { return AL::kmajor ? e % KQ : e / BM; };
+    auto b_row = [&](int e) { return BL::kmajor ? e / KQ : e % BN; };
+    auto b_quad = [&](int e) { return BL::kmajor ? e % KQ : e / BN; };
 
-    typename AL::State ast[A_STATES];
-    typename BL::State bst[B_STATES];
-    bool aok[A_STATES], bok[B_STATES];
+    typename AL::State ast[A_ITEMS];
+    typename BL::State bst[B_ITEMS];
+    bool aok[A_ITEMS], bok[B_ITEMS];
 #pragma unroll
-    for (int it = 0; it < A_STATES; ++it) {
+    for (int it = 0; it < A_ITEMS; ++it) {
         int e = tid + it * GEMM_THREADS;
-        int lr = AL::kmajor ? e / KQ : e % BM;
-        bool in_tile = AL::kmajor ? (e < BM * BK / 4) : (e < BM * BK);
-        int pr = in_tile ? phys_row(lr) : -1;
+        int pr = e < BM * KQ ? phys_row(a_row(e)) : -1;
         aok[it] = pr >= 0;
         ast[it] = al.setup(z, aok[it] ? pr : 0);
     }
 #pragma unroll
-    for (int it = 0; it < B_STATES; ++it) {
+    for (int it = 0; it < B_ITEMS; ++it) {
         int e = tid + it * GEMM_THREADS;
-        int lc = BL::kmajor ? e / KQ : e % BN;
-        bool in_tile = BL::kmajor ? (e < BN * BK / 4) : (e < BN * BK);
-        int n = n0 + lc;
-        bok[it] = in_tile && n < N;
+        int n = n0 + b_row(e);
+        bok[it] = e < BN * KQ && n < N;
         bst[it] = bl.setup(z, bok[it] ? n : 0);
     }
 
-    float areg[A_REGS], breg[B_REGS];
-
-    auto load_tiles = [&](int k0) {
-#pragma unroll
-        for (int it = 0; it < A_STATES; ++it) {
-            int e = tid + it * GEMM_THREADS;
-            if constexpr (AL::kmajor) {
-                int k = k0 + 4 * (e % KQ);
-                float4 v = aok[it] ? al.load4(ast[it], k, K) : make_float4(0.f, 0.f, 0.f, 0.f);
-                areg[4 * it + 0] = v.x;
-                areg[4 * it + 1] = v.y;
-                areg[4 * it + 2] = v.z;
-                areg[4 * it + 3] = v.w;
-            } else {
-                int k = k0 + e / BM;
-                areg[it] = (aok[it] && k < K) ? al.load(ast[it], k) : 0.0f;
-            }
-        }
-#pragma unroll
-        for (int it = 0; it < B_STATES; ++it) {
-            int e = tid + it * GEMM_THREADS;
-            if constexpr (BL::kmajor) {
-                int k = k0 + 4 * (e % KQ);
-                float4 v = bok[it] ? bl.load4(bst[it], k, K) : make_float4(0.f, 0.f, 0.f, 0.f);
-                breg[4 * it + 0] = v.x;
-                breg[4 * it + 1] = v.y;
-                breg[4 * it + 2] = v.z;
-                breg[4 * it + 3] = v.w;
-            } else {
-                int k = k0 + e / BN;
-                breg[it] = (bok[it] && k < K) ? bl.load(bst[it], k) : 0.0f;
-            }
+    float4 areg[A_ITEMS], breg[B_ITEMS];
+    auto fetch = [&](const auto &ld, const auto &st, bool ok, int k) -> float4 {
+        using L = std::decay_t<decltype(ld)>;
+        if (!ok) return make_float4(0.f, 0.f, 0.f, 0.f);
+        if constexpr (L::kmajor) {
+            return ld.load4(st, k, K);
+        } else {
+            float4 v;
+            v.x = k < K ? ld.load(st, k) : 0.f;
+            v.y = k + 1 < K ? ld.load(st, k + 1) : 0.f;
+            v.z = k + 2 < K ? ld.load(st, k + 2) : 0.f;
+            v.w = k + 3 < K ? ld.load(st, k + 3) : 0.f;
+            return v;
         }
     };
-
+    auto load_tiles = [&](int k0) {
+#pragma unroll
+        for (int it = 0; it < A_ITEMS; ++it)
+            areg[it] = fetch(al, ast[it], aok[it], k0 + 4 * a_quad(tid + it * GEMM_THREADS));
+#pragma unroll
+        for (int it = 0; it < B_ITEMS; ++it)
+            breg[it] = fetch(bl, bst[it], bok[it], k0 + 4 * b_quad(tid + it * GEMM_THREADS));
+    };
     auto store_tiles = [&](int buf) {
 #pragma unroll
-        for (int it = 0; it < A_STATES; ++it) {
+        for (int it = 0; it < A_ITEMS; ++it) {
             int e = tid + it * GEMM_THREADS;
-            if constexpr (AL::kmajor) {
-                if (e < BM * BK / 4) {
-                    int lr = e / KQ, kk = 4 * (e % KQ);
-#pragma unroll
-                    for (int j = 0; j < 4; ++j) As[buf][kk + j][lr] = areg[4 * it + j];
-                }
-            } else {
-                if (e < BM * BK) As[buf][e / BM][e % BM] = areg[it];
-            }
+            if (e < BM * KQ) *reinterpret_cast<float4 *>(&As[buf][a_row(e)][4 * a_quad(e)]) = areg[it];
         }
 #pragma unroll
-        for (int it = 0; it < B_STATES; ++it) {
+        for (int it = 0; it < B_ITEMS; ++it) {
             int e = tid + it * GEMM_THREADS;
-            if constexpr (BL::kmajor) {
-                if (e < BN * BK / 4) {
-                    int lc = e / KQ, kk = 4 * (e % KQ);
-#pragma unroll
-                    for (int j = 0; j < 4; ++j) Bs[buf][kk + j][lc] = breg[4 * it + j];
-                }
-            } else {
-                if (e < BN * BK) Bs[buf][e / BN][e % BN] = breg[it];
-            }
+            if (e < BN * KQ) *reinterpret_cast<float4 *>(&Bs[buf][b_row(e)][4 * b_quad(e)]) = breg[it];
         }
     };
 
@@ -190,17 +160,21 @@ __global__ __launch_bounds__(GEMM_THREADS) void gemm_kernel(int M, int N, int K,
         const int cur = kt & 1;
         if (kt + 1 < nk) load_tiles((kt + 1) * BK);
 #pragma unroll
-        for (int s = 0; s < BK / 2; ++s) {
-            float a[TM], b[TN];
-#pragma unroll
-            for (int i = 0; i < TM; ++i) a[i] = As[cur][2 * s + khalf][wm * WTM + i * 32 + row_in];
-#pragma unroll
-            for (int j = 0; j < TN; ++j) b[j] = Bs[cur][2 * s + khalf][wn * WTN + j * 32 + row_in];
+        for (int g = 0; g < BK / 8; ++g) {
+            floatx4 a[TM], b[TN];
 #pragma unroll
             for (int i = 0; i < TM; ++i)
+                a[i] = *reinterpret_cast<const floatx4 *>(&As[cur][wm * WTM + i * 32 + row_in][8 * g + 4 * khalf]);
 #pragma unroll
-                for (int j = 0; j < TN; ++j)
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[i], b[j], acc[i][j], 0, 0, 0);
+            for (int j = 0; j < TN; ++j)
+                b[j] = *reinterpret_cast<const floatx4 *>(&Bs[cur][wn * WTN + j * 32 + row_in][8 * g + 4 * khalf]);
+#pragma unroll
+            for (int t = 0; t < 4; ++t)
+#pragma unroll
+                for (int i = 0; i < TM; ++i)
+#pragma unroll
+                    for (int j = 0; j < TN; ++j)
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[i][t], b[j][t], acc[i][j], 0, 0, 0);
         }
         if (kt + 1 < nk) store_tiles(cur ^ 1);
         __syncthreads();

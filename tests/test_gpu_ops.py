@@ -198,6 +198,29 @@ def test_attention_matches_oracle(lib, oracle, batch, heads, nq, nk):
     assert rms_relative_error(ref, out.cpu().numpy()) < 1e-5
 
 
+@pytest.mark.parametrize("ramp", [1.0, 3.0, -3.0])
+def test_attention_running_max_moves_across_tiles(lib, oracle, ramp):
+    """Key norms ramp along the sequence, so each query's row max keeps rising
+    (or falls after the first tile) by many times 2^8 in probability: every
+    rescale path of the online softmax runs, and the last tile is ragged."""
+    r = rng(77)
+    nq, nk, heads = 150, 700, 2
+    D = heads * 64
+    q = r.uniform(-2, 2, (1, nq, D)).astype(np.float32)
+    gain = np.exp(ramp * np.linspace(0.0, 1.0, nk, dtype=np.float32))[None, :, None]
+    k = (r.uniform(-2, 2, (1, nk, D)) * gain).astype(np.float32)
+    v = r.uniform(-2, 2, (1, nk, D)).astype(np.float32)
+    ref = np.empty_like(q)
+    for h in range(heads):
+        sl = slice(64 * h, 64 * h + 64)
+        ref[0, :, sl] = oracle.attention_head(q[0, :, sl], k[0, :, sl], v[0, :, sl], 0.125)
+    out = torch.empty(q.shape, device="cuda")
+    dq, dk, dv = dev(q), dev(k), dev(v)
+    call(lib, "dmx_op_attention", stream(), ptr(dq), ptr(dk), ptr(dv), ptr(out), 1, heads, nq, nk,
+         ctypes.c_float(0.125))
+    assert rms_relative_error(ref, out.cpu().numpy()) < 1e-5
+
+
 def test_layer_norm_matches_oracle(lib, oracle):
     r = rng(1)
     x = r.uniform(-3, 3, (333, 512)).astype(np.float32)
