@@ -186,6 +186,18 @@ def main():
     if not np.isfinite(d_stems.abs().sum().item()):
         raise RuntimeError("non-finite stems")
 
+    # The same separation from host arrays to host stems (dmx_separate: the
+    # mix upload and the stem readback are inside the timing), after one
+    # untimed run. Reported beside `value`, never as it.
+    host_opts = pkg.SeparateOptions(shifts=0, overlap=0.25, batch_chunks=args.batch_chunks)
+    left, right = np.ascontiguousarray(mix[0]), np.ascontiguousarray(mix[1])
+    pkg.separate_runners([runner], left, right, cfg.samplerate, host_opts)
+    t0 = time.perf_counter()
+    pkg.separate_runners([runner], left, right, cfg.samplerate, host_opts)
+    host_s = time.perf_counter() - t0
+    host_io = {"x_realtime": round(audio_s / host_s, 2), "ms": round(1000.0 * host_s, 2),
+               "note": "host f32 mix in, host f32 stems out (dmx_separate); one run after a warm-up"}
+
     attn_ms, attn_flops = attention_roofline(pkg, torch, args.batch_chunks, args.attn_iters)
     attn_tflops = attn_flops / (attn_ms * 1e-3) / 1e12
     roofline = {"bound": "mfma", "achieved": round(attn_tflops, 2), "peak": FP32_MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
@@ -211,6 +223,7 @@ def main():
                                "mix and stems resident in HBM",
                    "segment_samples": cfg.training_length, "batch_chunks": args.batch_chunks},
         "cross_attn_tflops": round(attn_tflops, 2),
+        "host_io": host_io,
         "roofline": roofline,
         "cpu_baseline": None if args.no_cpu_baseline else cpu_baseline(pkg),
     }

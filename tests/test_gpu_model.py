@@ -160,3 +160,57 @@ def test_full_segment_forward_matches_oracle(dmx, oracle):
     ref = oracle.Model(weights, cfg).forward(mix)
     snrs = per_stem_snr(ref, out)
     assert min(snrs) >= 60.0, snrs
+
+
+def test_forward_matches_the_golden_fixture(dmx):
+    """The HIP forward against the committed float64-torch fixture directly
+    (no oracle in the loop): stems and sampled named activations."""
+    from test_golden import check_fingerprints, golden, l4096_config
+    g = golden("htdemucs_L4096_seed0.npz")
+    cfg = l4096_config(dmx)
+    runner = dmx.Runner(dmx.random_init(0, cfg), cfg)
+    trace = {}
+    runner.set_trace(None, lambda n, a: trace.__setitem__(n, a))
+    try:
+        out = runner.forward(g["mix"])
+    finally:
+        runner.set_trace(None, None)
+    snrs = per_stem_snr(g["stems"], out)
+    assert min(snrs) >= 60.0, snrs
+    check_fingerprints(g, trace, 1e-3)
+
+
+def _device_transformer(dmx, runner, x, xt):
+    import torch
+    b, d, f, t = x.shape
+    dx, dxt = torch.from_numpy(x).cuda(), torch.from_numpy(xt).cuda()
+    ox, oxt = torch.empty_like(dx), torch.empty_like(dxt)
+    torch.cuda.synchronize()
+    runner.crosstransformer_device(dx.data_ptr(), dxt.data_ptr(), b, f, t, xt.shape[-1], ox.data_ptr(), oxt.data_ptr())
+    runner.synchronize()
+    return ox.cpu().numpy(), oxt.cpu().numpy()
+
+
+def test_crosstransformer_matches_the_golden_stack(dmx):
+    """dmx_crosstransformer_device (config 2's entry point) on the fixture's
+    4x6 + 12 tokens, Xavier-init seed 2."""
+    from test_golden import golden
+    g = golden("transformer_F4T6_seed2.npz")
+    cfg = dmx.Config()
+    runner = dmx.Runner(dmx.xavier_transformer_init(2, cfg), cfg)
+    xo, xto = _device_transformer(dmx, runner, g["x"], g["xt"])
+    assert snr_db(g["out"], xo) >= 60.0 and snr_db(g["out_t"], xto) >= 60.0
+
+
+def test_crosstransformer_full_token_count_matches_oracle(dmx, oracle):
+    """BASELINE config 2 at batch 1: 2688 frequency tokens (8 x 336) and 1344
+    time tokens, N(0, 1) activations, Xavier-init transformer."""
+    cfg = dmx.Config()
+    w = dmx.xavier_transformer_init(2, cfg)
+    r = np.random.default_rng(21)
+    x = r.normal(size=(1, 512, 8, 336)).astype(np.float32)
+    xt = r.normal(size=(1, 512, 1344)).astype(np.float32)
+    xo, xto = _device_transformer(dmx, dmx.Runner(w, cfg), x, xt)
+    ro, rto = oracle.Model(w, cfg).transformer(x, xt)
+    assert snr_db(ro, xo) >= 60.0 and snr_db(rto, xto) >= 60.0
+    assert float(np.abs(ro - xo).max()) <= 1e-3 * max(1.0, float(np.abs(ro).max()))

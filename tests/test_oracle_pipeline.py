@@ -67,3 +67,22 @@ def test_a_linear_forward_commutes_with_the_overlap_add(dmx, oracle):
     for s in range(4):
         expect = (ident[s] - m) * (s + 1) + m
         assert snr_db(expect, single[s]) > 100
+
+
+def test_a_bag_is_the_weight_normalised_sum_of_its_networks(dmx, oracle):
+    """BagCombine (crates/demucs-core/src/api.rs:319-371, :883-971): stem s of
+    a bag is sum_n w[n][s] * y_n[s] / sum_n w[n][s]; with a one-hot matrix it
+    is exactly one network's separation (core/tests/api_facade.rs:233-272)."""
+    from conftest import small_config
+    cfg = small_config(dmx, 11025)
+    models = [oracle.Model(dmx.random_init(seed, cfg), cfg) for seed in (1, 2)]
+    mix = dmx.signals.synthetic_mix(5, 0.7)
+    opts = dmx.SeparateOptions(shifts=0, batch_chunks=2)
+    single = [oracle.separate([m], mix[0], mix[1], 44100, opts) for m in models]
+    bag = np.array([[1.0, 0.25, 0.0, 2.0], [0.0, 0.75, 1.0, 1.0]], np.float32)
+    both = oracle.separate(models, mix[0], mix[1], 44100, opts, bag_weights=bag)
+    for s in range(4):
+        expect = (bag[0, s] * single[0][s].astype(np.float64) + bag[1, s] * single[1][s]) / bag[:, s].sum()
+        assert snr_db(expect, both[s]) > 100.0, s
+    np.testing.assert_array_equal(both[0], single[0][0])
+    np.testing.assert_array_equal(both[2], single[1][2])
