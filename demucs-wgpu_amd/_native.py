@@ -74,6 +74,7 @@ SIGNATURES = {
     "dmx_op_group_norm": (_I, [_VP, _VP, _I, _I, _I, _I, _VP, _VP, _VP]),
     "dmx_op_glu": (_I, [_VP, _VP, _I, _I, _I, _VP]),
     "dmx_op_gelu": (_I, [_VP, _VP, _I64, _VP]),
+    "dmx_op_set_precision": (_I, [_I]),
     "dmx_op_spec_normalise": (_I, [_VP, _VP, _I, _I, _VP, _VP, _VP]),
     "dmx_op_ispec_sum": (_I, [_VP, _VP, _VP, _I, _I, _VP, _VP]),
 }

@@ -230,6 +230,186 @@ void attention_kernel(const float *__restrict__ q, int64_t ldq, const float *__r
     }
 }
 
+// ---------------------------------------------------------------------------
+// bf16-MFMA variant: Q, K, V and P enter v_mfma_f32_32x32x16_bf16 rounded to
+// bf16; scores, softmax, the running max/sum and O stay fp32. Same layout as
+// the fp32 kernel with 16-deep contractions: per 64-key tile, 8 MFMAs for
+// S^T = K Q^T and 8 for O^T += V^T P^T. The score registers 8m .. 8m+7 of a
+// lane (keys 16m + 8(e/4) + 4*half + e%4) are exactly one bf16x8 B operand, so
+// V^T is read as two 4-key runs per operand.
+// ---------------------------------------------------------------------------
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef float floatx8 __attribute__((ext_vector_type(8)));
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+
+constexpr int ATT_LDK16 = 72;  // bf16 per K row (144 B: 16-byte aligned, conflict-free b128 reads)
+constexpr int ATT_LDV16 = 68;  // bf16 per V^T row (136 B: conflict-free b64 reads)
+
+__device__ __forceinline__ bf16x8 to_bf16x8(floatx8 v) { return __builtin_convertvector(v, bf16x8); }
+
+__global__ __launch_bounds__(256) void attention_bf16_kernel(const float *__restrict__ q, int64_t ldq,
+                                                             const float *__restrict__ k, int64_t ldk,
+                                                             const float *__restrict__ v, int64_t ldv,
+                                                             float *__restrict__ out, int64_t ldo, int n_q, int n_k,
+                                                             float scale, int64_t q_bs, int64_t kv_bs, int64_t o_bs) {
+    __shared__ __align__(16) __bf16 Ks[2][ATT_KT][ATT_LDK16];  // [buffer][key][d]
+    __shared__ __align__(16) __bf16 Vt[2][ATT_D][ATT_LDV16];   // [buffer][d][key]
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int head = blockIdx.y, b = blockIdx.z;
+    const int j = lane & 31, half = lane >> 5;
+    const int qi = blockIdx.x * (ATT_QW * ATT_WAVES) + wave * ATT_QW + j;
+    const bool q_ok = qi < n_q;
+
+    const float *qb = q + b * q_bs + head * ATT_D;
+    const float *kb = k + b * kv_bs + head * ATT_D;
+    const float *vb = v + b * kv_bs + head * ATT_D;
+
+    // Q fragments: dims 16t + 8*half .. +7, pre-scaled into log2 units.
+    bf16x8 qf[4];
+    {
+        const float qs = scale * ATT_LOG2E;
+        const float *row = qb + (int64_t)(q_ok ? qi : 0) * ldq + 8 * half;
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            floatx8 x = {};
+            if (q_ok) {
+                const float4 a = *reinterpret_cast<const float4 *>(row + 16 * t);
+                const float4 c = *reinterpret_cast<const float4 *>(row + 16 * t + 4);
+                x = (floatx8){a.x, a.y, a.z, a.w, c.x, c.y, c.z, c.w};
+            }
+            qf[t] = to_bf16x8(x * qs);
+        }
+    }
+
+    float4 kpre[4], vpre[4];
+    auto slot_key = [&](int i) { return 16 * ((4 * wave + i) & 3) + (lane & 15); };
+    auto slot_d4 = [&](int i) { return 4 * ((4 * wave + i) >> 2) + (lane >> 4); };
+    auto fetch = [&](int key0) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int kk = key0 + slot_key(i), d = 4 * slot_d4(i);
+            if (kk < n_k) {
+                kpre[i] = *reinterpret_cast<const float4 *>(kb + (int64_t)kk * ldk + d);
+                vpre[i] = *reinterpret_cast<const float4 *>(vb + (int64_t)kk * ldv + d);
+            } else {
+                kpre[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+                vpre[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+            }
+        }
+    };
+    auto stage = [&](int buf) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int key = slot_key(i), d = 4 * slot_d4(i);
+            const bf16x4 kv = __builtin_convertvector((floatx4){kpre[i].x, kpre[i].y, kpre[i].z, kpre[i].w}, bf16x4);
+            *reinterpret_cast<bf16x4 *>(&Ks[buf][key][d]) = kv;
+            const bf16x4 vv = __builtin_convertvector((floatx4){vpre[i].x, vpre[i].y, vpre[i].z, vpre[i].w}, bf16x4);
+            Vt[buf][d + 0][key] = vv[0];
+            Vt[buf][d + 1][key] = vv[1];
+            Vt[buf][d + 2][key] = vv[2];
+            Vt[buf][d + 3][key] = vv[3];
+        }
+    };
+    // V^T operand for dim row d and keys base + 8(e/4) + 4*half + e%4.
+    auto vfrag = [&](int buf, int d, int base) -> bf16x8 {
+        const bf16x4 lo = *reinterpret_cast<const bf16x4 *>(&Vt[buf][d][base + 4 * half]);
+        const bf16x4 hi = *reinterpret_cast<const bf16x4 *>(&Vt[buf][d][base + 8 + 4 * half]);
+        return (bf16x8){lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+    };
+
+    const floatx16 zero = {};
+    floatx16 o0 = zero, o1 = zero;
+    float m_run = -INFINITY, l_run = 0.0f;
+
+    auto tile = [&](auto mask_tag, int buf, int key0) {
+        constexpr bool MASK = decltype(mask_tag)::value;
+        floatx16 s0 = zero, s1 = zero;
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            const bf16x8 ka = *reinterpret_cast<const bf16x8 *>(&Ks[buf][j][16 * t + 8 * half]);
+            const bf16x8 kc = *reinterpret_cast<const bf16x8 *>(&Ks[buf][32 + j][16 * t + 8 * half]);
+            s0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ka, qf[t], s0, 0, 0, 0);
+            s1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kc, qf[t], s1, 0, 0, 0);
+        }
+        if constexpr (MASK) {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int kk = key0 + 8 * (r >> 2) + 4 * half + (r & 3);
+                if (kk >= n_k) s0[r] = -INFINITY;
+                if (kk + 32 >= n_k) s1[r] = -INFINITY;
+            }
+        }
+        float mloc = fmaxf(s0[0], s1[0]);
+#pragma unroll
+        for (int r = 1; r < 16; ++r) mloc = fmaxf(mloc, fmaxf(s0[r], s1[r]));
+        mloc = fmaxf(mloc, __shfl_xor(mloc, 32, 64));
+        if (__any(mloc > m_run + ATT_SLACK)) {
+            const float m_new = fmaxf(m_run, mloc);
+            const float corr = __builtin_amdgcn_exp2f(m_run - m_new);
+            l_run *= corr;
+            m_run = m_new;
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                o0[r] *= corr;
+                o1[r] *= corr;
+            }
+        }
+        float lsum = 0.0f;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            s0[r] = __builtin_amdgcn_exp2f(s0[r] - m_run);
+            s1[r] = __builtin_amdgcn_exp2f(s1[r] - m_run);
+            lsum += s0[r] + s1[r];
+        }
+        lsum += __shfl_xor(lsum, 32, 64);
+        l_run += lsum;
+#pragma unroll
+        for (int m = 0; m < 2; ++m) {
+            const bf16x8 p0 = to_bf16x8((floatx8){s0[8 * m], s0[8 * m + 1], s0[8 * m + 2], s0[8 * m + 3],
+                                                  s0[8 * m + 4], s0[8 * m + 5], s0[8 * m + 6], s0[8 * m + 7]});
+            const bf16x8 p1 = to_bf16x8((floatx8){s1[8 * m], s1[8 * m + 1], s1[8 * m + 2], s1[8 * m + 3],
+                                                  s1[8 * m + 4], s1[8 * m + 5], s1[8 * m + 6], s1[8 * m + 7]});
+            o0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vfrag(buf, j, 16 * m), p0, o0, 0, 0, 0);
+            o1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vfrag(buf, 32 + j, 16 * m), p0, o1, 0, 0, 0);
+            o0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vfrag(buf, j, 32 + 16 * m), p1, o0, 0, 0, 0);
+            o1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vfrag(buf, 32 + j, 32 + 16 * m), p1, o1, 0, 0, 0);
+        }
+    };
+
+    const int tiles = (n_k + ATT_KT - 1) / ATT_KT;
+    const bool ragged = (n_k % ATT_KT) != 0;
+    fetch(0);
+    stage(0);
+    __syncthreads();
+    for (int t = 0; t < tiles; ++t) {
+        const int buf = t & 1;
+        const bool more = t + 1 < tiles;
+        if (more) fetch((t + 1) * ATT_KT);
+        if (!more && ragged)
+            tile(std::true_type{}, buf, t * ATT_KT);
+        else
+            tile(std::false_type{}, buf, t * ATT_KT);
+        if (more) {
+            stage(buf ^ 1);
+            __syncthreads();
+        }
+    }
+
+    if (!q_ok) return;
+    const float inv = l_run > 0.0f ? 1.0f / l_run : 1.0f;
+    float *orow = out + b * o_bs + (int64_t)qi * ldo + head * ATT_D;
+#pragma unroll
+    for (int a = 0; a < 4; ++a) {
+        float4 w0 = make_float4(o0[4 * a] * inv, o0[4 * a + 1] * inv, o0[4 * a + 2] * inv, o0[4 * a + 3] * inv);
+        float4 w1 = make_float4(o1[4 * a] * inv, o1[4 * a + 1] * inv, o1[4 * a + 2] * inv, o1[4 * a + 3] * inv);
+        *reinterpret_cast<float4 *>(orow + 8 * a + 4 * half) = w0;
+        *reinterpret_cast<float4 *>(orow + 32 + 8 * a + 4 * half) = w1;
+    }
+}
+
 }  // namespace
 
 void attention(hipStream_t s, const float *q, int64_t ldq, const float *k, int64_t ldk, const float *v, int64_t ldv,
@@ -246,8 +426,12 @@ void attention(hipStream_t s, const float *q, int64_t ldq, const float *k, int64
                  15) == 0,
                 "attention: operands must be 16-byte aligned");
     dim3 grid((unsigned)ceil_div(n_q, ATT_QW * ATT_WAVES), (unsigned)heads, (unsigned)batch);
-    hipLaunchKernelGGL(attention_kernel, grid, dim3(256), 0, s, q, ldq, k, ldk, v, ldv, out, ldo, n_q, n_k, scale,
-                       q_batch_stride, kv_batch_stride, out_batch_stride);
+    if (mfma_precision() == MfmaPrecision::BF16)
+        hipLaunchKernelGGL(attention_bf16_kernel, grid, dim3(256), 0, s, q, ldq, k, ldk, v, ldv, out, ldo, n_q, n_k,
+                           scale, q_batch_stride, kv_batch_stride, out_batch_stride);
+    else
+        hipLaunchKernelGGL(attention_kernel, grid, dim3(256), 0, s, q, ldq, k, ldk, v, ldv, out, ldo, n_q, n_k, scale,
+                           q_batch_stride, kv_batch_stride, out_batch_stride);
     DMX_LAUNCH_CHECK();
 }
 

@@ -123,6 +123,13 @@ int dmx_op_glu(void *stream, const float *x, int b, int c2, int inner, float *ou
     return guarded([&] { glu(as_stream(stream), x, b, c2, inner, out); });
 }
 
+int dmx_op_set_precision(int precision) {
+    return guarded([&] {
+        DMX_REQUIRE(precision == DMX_PRECISION_FP32 || precision == DMX_PRECISION_BF16, "unknown precision");
+        mfma_precision() = precision == DMX_PRECISION_BF16 ? MfmaPrecision::BF16 : MfmaPrecision::FP32;
+    });
+}
+
 int dmx_op_gelu(void *stream, const float *x, int64_t n, float *out) {
     return guarded([&] { gelu(as_stream(stream), x, n, out); });
 }

@@ -45,6 +45,22 @@ inline void require_ptrs(std::initializer_list<const void *> ptrs, const char *w
 // The calling thread's last error message (dmx_last_error).
 std::string &last_error_slot();
 
+// Input precision of the MFMA contractions (GEMMs, attention) that the
+// calling thread launches. The runner sets it per call from its precision;
+// accumulation, softmax, norms and outputs are fp32 either way.
+enum class MfmaPrecision { FP32, BF16 };
+inline MfmaPrecision &mfma_precision() {
+    static thread_local MfmaPrecision p = MfmaPrecision::FP32;
+    return p;
+}
+struct MfmaPrecisionScope {
+    MfmaPrecision prev;
+    explicit MfmaPrecisionScope(MfmaPrecision p) : prev(mfma_precision()) { mfma_precision() = p; }
+    ~MfmaPrecisionScope() { mfma_precision() = prev; }
+    MfmaPrecisionScope(const MfmaPrecisionScope &) = delete;
+    MfmaPrecisionScope &operator=(const MfmaPrecisionScope &) = delete;
+};
+
 // Runs f, turning exceptions into a dmx_status code and a message.
 template <class F>
 int guarded(F &&f) {

@@ -268,26 +268,36 @@ struct EpLinear {
 // Tile selection
 // ---------------------------------------------------------------------------
 
-template <bool GLU, class AL, class BL, class EP>
-void gemm_auto(hipStream_t s, int M, int N, int K, int batches, const AL &al, const BL &bl, const EP &ep) {
+template <bool GLU, bool BF16, class AL, class BL, class EP>
+void gemm_pick(hipStream_t s, int M, int N, int K, int batches, const AL &al, const BL &bl, const EP &ep) {
     if constexpr (GLU) {
         if (M > 32)
-            launch_gemm<128, 128, 2, true>(s, M, N, K, batches, al, bl, ep);
+            launch_gemm<128, 128, 2, true, BF16>(s, M, N, K, batches, al, bl, ep);
         else
-            launch_gemm<64, 128, 1, true>(s, M, N, K, batches, al, bl, ep);
+            launch_gemm<64, 128, 1, true, BF16>(s, M, N, K, batches, al, bl, ep);
     } else {
 #ifdef DMX_BIG_BM  // tuning builds only: a larger tile for tall problems
         if (M >= DMX_BIG_BM)
-            launch_gemm<DMX_BIG_BM, DMX_BIG_BN, DMX_BIG_WM, false>(s, M, N, K, batches, al, bl, ep);
+            launch_gemm<DMX_BIG_BM, DMX_BIG_BN, DMX_BIG_WM, false, BF16>(s, M, N, K, batches, al, bl, ep);
         else
 #endif
         if (M >= 96)
-            launch_gemm<128, 128, 2, false>(s, M, N, K, batches, al, bl, ep);
+            launch_gemm<128, 128, 2, false, BF16>(s, M, N, K, batches, al, bl, ep);
         else if (M > 32)
-            launch_gemm<64, 128, 2, false>(s, M, N, K, batches, al, bl, ep);
+            launch_gemm<64, 128, 2, false, BF16>(s, M, N, K, batches, al, bl, ep);
         else
-            launch_gemm<32, 256, 1, false>(s, M, N, K, batches, al, bl, ep);
+            launch_gemm<32, 256, 1, false, BF16>(s, M, N, K, batches, al, bl, ep);
     }
+}
+
+// Contractions take bf16 MFMA inputs when the calling thread's precision
+// scope says so (fp32 accumulation and epilogues either way).
+template <bool GLU, class AL, class BL, class EP>
+void gemm_auto(hipStream_t s, int M, int N, int K, int batches, const AL &al, const BL &bl, const EP &ep) {
+    if (mfma_precision() == MfmaPrecision::BF16)
+        gemm_pick<GLU, true>(s, M, N, K, batches, al, bl, ep);
+    else
+        gemm_pick<GLU, false>(s, M, N, K, batches, al, bl, ep);
 }
 
 bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
@@ -519,7 +529,9 @@ void tokens_to_channels(hipStream_t s, const float *tok, int b, int F, int T, in
     ep.batch_stride = (int64_t)M * F * T;
     ep.N = F * T;
     ep.act = ACT_NONE;
-    gemm_auto<false>(s, M, F * T, D, b, kmajor(w, D, 0), TokenGather{tok, F, T, D}, ep);
+    // A rearrange (w is the identity in the transformer-only path): kept in
+    // fp32 whatever the precision scope, so it stays exact.
+    gemm_pick<false, false>(s, M, F * T, D, b, kmajor(w, D, 0), TokenGather{tok, F, T, D}, ep);
 }
 
 }  // namespace dmx

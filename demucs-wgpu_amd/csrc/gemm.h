@@ -38,27 +38,51 @@ namespace dmx {
 
 typedef float floatx16 __attribute__((ext_vector_type(16)));
 typedef float floatx4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 
-// k-tile depth.
+// k-tile depth of the fp32 kernel (the bf16 kernel stages 32).
 #ifndef DMX_GEMM_BK
 #define DMX_GEMM_BK 16
 #endif
 constexpr int GEMM_BK = DMX_GEMM_BK;
 constexpr int GEMM_THREADS = 256;
 
-template <int BM, int BN, int WAVES_M, bool GLU, class AL, class BL, class EP>
+// Round-to-nearest-even fp32 -> bf16 of four values (two v_cvt_pk_bf16_f32).
+__device__ __forceinline__ uint2 pack_bf16x4(float4 v) {
+    typedef float f2 __attribute__((ext_vector_type(2)));
+    typedef __bf16 b2 __attribute__((ext_vector_type(2)));
+    const b2 lo = __builtin_convertvector((f2){v.x, v.y}, b2);
+    const b2 hi = __builtin_convertvector((f2){v.z, v.w}, b2);
+    return make_uint2(__builtin_bit_cast(unsigned, lo), __builtin_bit_cast(unsigned, hi));
+}
+
+// Stage element type and depth: fp32 stages BK = 16 floats per row; bf16
+// stages 32 (one v_mfma_f32_32x32x16_bf16 per 16, operands 8 bf16 per lane).
+template <bool BF16>
+struct GemmStage {
+    using T = float;
+    static constexpr int BK = GEMM_BK;
+};
+template <>
+struct GemmStage<true> {
+    using T = unsigned short;
+    static constexpr int BK = 32;
+};
+
+template <int BM, int BN, int WAVES_M, bool GLU, bool BF16, class AL, class BL, class EP>
 __global__ __launch_bounds__(GEMM_THREADS) void gemm_kernel(int M, int N, int K, AL al, BL bl, EP ep) {
-    constexpr int BK = GEMM_BK;
-    constexpr int KQ = BK / 4;   // float4 chunks per row of a stage
-    constexpr int LD = BK + 4;   // LDS row stride (floats)
+    using T = typename GemmStage<BF16>::T;
+    constexpr int BK = GemmStage<BF16>::BK;
+    constexpr int KQ = BK / 4;                  // 4-k chunks per row of a stage
+    constexpr int LD = BK + 16 / (int)sizeof(T);  // LDS row stride: 16 bytes of padding
     static_assert(BK % 8 == 0, "BK must be a multiple of 8");
     constexpr int WAVES_N = 4 / WAVES_M;
     constexpr int WTM = BM / WAVES_M, WTN = BN / WAVES_N;
     constexpr int TM = WTM / 32, TN = WTN / 32;
     static_assert(TM >= 1 && TN >= 1, "wave tile must hold at least one 32x32 MFMA tile");
     static_assert(!GLU || TM == 2, "GLU needs exactly one value and one gate tile per wave");
-    __shared__ __align__(16) float As[2][BM][LD];
-    __shared__ __align__(16) float Bs[2][BN][LD];
+    __shared__ __align__(16) T As[2][BM][LD];
+    __shared__ __align__(16) T Bs[2][BN][LD];
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int wm = wave % WAVES_M, wn = wave / WAVES_M;
@@ -130,16 +154,22 @@ __global__ __launch_bounds__(GEMM_THREADS) void gemm_kernel(int M, int N, int K,
         for (int it = 0; it < B_ITEMS; ++it)
             breg[it] = fetch(bl, bst[it], bok[it], k0 + 4 * b_quad(tid + it * GEMM_THREADS));
     };
+    auto put = [&](T *dst, const float4 &v) {
+        if constexpr (BF16)
+            *reinterpret_cast<uint2 *>(dst) = pack_bf16x4(v);
+        else
+            *reinterpret_cast<float4 *>(dst) = v;
+    };
     auto store_tiles = [&](int buf) {
 #pragma unroll
         for (int it = 0; it < A_ITEMS; ++it) {
             int e = tid + it * GEMM_THREADS;
-            if (e < BM * KQ) *reinterpret_cast<float4 *>(&As[buf][a_row(e)][4 * a_quad(e)]) = areg[it];
+            if (e < BM * KQ) put(&As[buf][a_row(e)][4 * a_quad(e)], areg[it]);
         }
 #pragma unroll
         for (int it = 0; it < B_ITEMS; ++it) {
             int e = tid + it * GEMM_THREADS;
-            if (e < BN * KQ) *reinterpret_cast<float4 *>(&Bs[buf][b_row(e)][4 * b_quad(e)]) = breg[it];
+            if (e < BN * KQ) put(&Bs[buf][b_row(e)][4 * b_quad(e)], breg[it]);
         }
     };
 
@@ -159,22 +189,41 @@ __global__ __launch_bounds__(GEMM_THREADS) void gemm_kernel(int M, int N, int K,
     for (int kt = 0; kt < nk; ++kt) {
         const int cur = kt & 1;
         if (kt + 1 < nk) load_tiles((kt + 1) * BK);
+        if constexpr (BF16) {
+            // Lane half h holds k = 16g + 8h .. +7 of its row for A and B alike.
 #pragma unroll
-        for (int g = 0; g < BK / 8; ++g) {
-            floatx4 a[TM], b[TN];
+            for (int g = 0; g < BK / 16; ++g) {
+                bf16x8 a[TM], b[TN];
 #pragma unroll
-            for (int i = 0; i < TM; ++i)
-                a[i] = *reinterpret_cast<const floatx4 *>(&As[cur][wm * WTM + i * 32 + row_in][8 * g + 4 * khalf]);
+                for (int i = 0; i < TM; ++i)
+                    a[i] = *reinterpret_cast<const bf16x8 *>(&As[cur][wm * WTM + i * 32 + row_in][16 * g + 8 * khalf]);
 #pragma unroll
-            for (int j = 0; j < TN; ++j)
-                b[j] = *reinterpret_cast<const floatx4 *>(&Bs[cur][wn * WTN + j * 32 + row_in][8 * g + 4 * khalf]);
-#pragma unroll
-            for (int t = 0; t < 4; ++t)
+                for (int j = 0; j < TN; ++j)
+                    b[j] = *reinterpret_cast<const bf16x8 *>(&Bs[cur][wn * WTN + j * 32 + row_in][16 * g + 8 * khalf]);
 #pragma unroll
                 for (int i = 0; i < TM; ++i)
 #pragma unroll
                     for (int j = 0; j < TN; ++j)
-                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[i][t], b[j][t], acc[i][j], 0, 0, 0);
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[i], b[j], acc[i][j], 0, 0, 0);
+            }
+        } else {
+#pragma unroll
+            for (int g = 0; g < BK / 8; ++g) {
+                floatx4 a[TM], b[TN];
+#pragma unroll
+                for (int i = 0; i < TM; ++i)
+                    a[i] = *reinterpret_cast<const floatx4 *>(&As[cur][wm * WTM + i * 32 + row_in][8 * g + 4 * khalf]);
+#pragma unroll
+                for (int j = 0; j < TN; ++j)
+                    b[j] = *reinterpret_cast<const floatx4 *>(&Bs[cur][wn * WTN + j * 32 + row_in][8 * g + 4 * khalf]);
+#pragma unroll
+                for (int t = 0; t < 4; ++t)
+#pragma unroll
+                    for (int i = 0; i < TM; ++i)
+#pragma unroll
+                        for (int j = 0; j < TN; ++j)
+                            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[i][t], b[j][t], acc[i][j], 0, 0, 0);
+            }
         }
         if (kt + 1 < nk) store_tiles(cur ^ 1);
         __syncthreads();
@@ -203,14 +252,14 @@ __global__ __launch_bounds__(GEMM_THREADS) void gemm_kernel(int M, int N, int K,
 }
 
 // Launches gemm_kernel on `stream` for `batches` independent problems.
-template <int BM, int BN, int WAVES_M, bool GLU, class AL, class BL, class EP>
+template <int BM, int BN, int WAVES_M, bool GLU, bool BF16 = false, class AL, class BL, class EP>
 void launch_gemm(hipStream_t stream, int M, int N, int K, int batches, const AL &al, const BL &bl, const EP &ep) {
     if (M <= 0 || N <= 0 || batches <= 0) return;
     const int m_per_block = GLU ? BM / 2 : BM;
     dim3 grid((unsigned)ceil_div(N, BN), (unsigned)ceil_div(M, m_per_block), (unsigned)batches);
     DMX_REQUIRE(grid.y <= 65535 && grid.z <= 65535, "GEMM grid too large");
-    hipLaunchKernelGGL((gemm_kernel<BM, BN, WAVES_M, GLU, AL, BL, EP>), grid, dim3(GEMM_THREADS), 0, stream, M, N,
-                       K, al, bl, ep);
+    hipLaunchKernelGGL((gemm_kernel<BM, BN, WAVES_M, GLU, BF16, AL, BL, EP>), grid, dim3(GEMM_THREADS), 0, stream, M,
+                       N, K, al, bl, ep);
     DMX_LAUNCH_CHECK();
 }
 

@@ -386,8 +386,14 @@ void transformer(dmx_runner &r, hipStream_t s, const float *x, const float *xt, 
 
 // Stack-only entry point: same prologue/layers, outputs rearranged back to
 // (B, D, F, T) / (B, D, Lt) without the channel mixers.
+// The runner's precision as the MFMA input precision of what it launches.
+MfmaPrecision mfma_of(const dmx_runner &r) {
+    return r.precision == DMX_PRECISION_BF16 ? MfmaPrecision::BF16 : MfmaPrecision::FP32;
+}
+
 void transformer_only(dmx_runner &r, hipStream_t s, const float *x, const float *xt, int B, int F, int T, int Lt,
                       float *x_out, float *xt_out) {
+    MfmaPrecisionScope prec(mfma_of(r));
     const int D = r.tch;
     const int64_t Lf = (int64_t)F * T;
     const float wpe = (float)r.cfg.t_weight_pos_embed;
@@ -422,6 +428,7 @@ void transformer_only(dmx_runner &r, hipStream_t s, const float *x, const float 
 
 // `Htdemucs::forward` on device: mix (B, 2, L) with L == training_length -> stems (B, S, 2, L).
 void forward_full(dmx_runner &r, hipStream_t s, const float *mix, int B, float *stems) {
+    MfmaPrecisionScope prec(mfma_of(r));
     const dmx_config &c = r.cfg;
     const int L = (int)r.training_length, nfft = c.nfft, hop = r.hop, le = (int)ceil_div(L, hop), bins = nfft / 2;
     DBuf frames = fbuf(s, (int64_t)B * 2 * le * bins * 2);
@@ -1026,8 +1033,6 @@ int dmx_runner_create(const dmx_tensor *weights, size_t n_weights, const dmx_con
         if (!weights || !cfg) throw_error(DMX_ERR_ARGUMENT, "null weights or config");
         if (precision != DMX_PRECISION_FP32 && precision != DMX_PRECISION_BF16)
             throw_error(DMX_ERR_ARGUMENT, "unknown precision");
-        if (precision == DMX_PRECISION_BF16)
-            throw_error(DMX_ERR_UNSUPPORTED, "the bf16 MFMA variant is not built yet");
         validate(*cfg);
         int count = 0;
         if (hipGetDeviceCount(&count) != hipSuccess || count == 0) throw_error(DMX_ERR_GPU, "no HIP device is visible");

@@ -20,6 +20,15 @@ extern "C" {
 #endif
 
 enum { DMX_ACT_NONE = 0, DMX_ACT_GELU = 1 };
+
+/* MFMA input precision (DMX_PRECISION_FP32 / DMX_PRECISION_BF16) of the
+ * contractions this thread enqueues through the dmx_op_* entry points below
+ * (linear, conv2d, conv2d_glu, conv_transpose, dconv_layer, pointwise,
+ * attention); accumulation and every output stay fp32. Per thread, default
+ * fp32. The bf16 variant of a runner is chosen at dmx_runner_create instead.
+ * No counterpart in the reference, whose device path is fp32 only; it exists
+ * so the bf16 kernels can be tested one at a time like the fp32 ones. */
+int dmx_op_set_precision(int precision);
 enum { DMX_TAIL_BIAS = 0, DMX_TAIL_BIAS_GELU = 1, DMX_TAIL_RESIDUAL_SCALE = 2 };
 
 /* conv2d_gemm_into (kernels.rs:3089-3257) as an implicit GEMM: x (b, ic, h, w),

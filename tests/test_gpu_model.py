@@ -214,3 +214,28 @@ def test_crosstransformer_full_token_count_matches_oracle(dmx, oracle):
     ro, rto = oracle.Model(w, cfg).transformer(x, xt)
     assert snr_db(ro, xo) >= 60.0 and snr_db(rto, xto) >= 60.0
     assert float(np.abs(ro - xo).max()) <= 1e-3 * max(1.0, float(np.abs(ro).max()))
+
+
+def test_bf16_forward_meets_the_40_db_gate(dmx, oracle):
+    """BASELINE config 5's check on two of its segments: the bf16-MFMA runner
+    (seed-7 weights, N(0, 0.1^2) input) against the fp32 oracle, per-stem
+    SNR >= 40 dB; and it really is the bf16 path (below fp32 agreement)."""
+    cfg = dmx.Config()
+    w = dmx.random_init(7, cfg)
+    mix = dmx.signals.gaussian_segments(7, 2, cfg.training_length)
+    out = dmx.Runner(w, cfg, precision=dmx.PRECISION_BF16).forward(mix)
+    ref = oracle.Model(w, cfg).forward(mix)
+    snrs = per_stem_snr(ref, out)
+    assert min(snrs) >= 40.0, snrs
+    assert max(snrs) < 100.0, snrs
+
+
+def test_bf16_separation_meets_the_40_db_gate(dmx, oracle, small):
+    cfg, weights, _, model = small
+    runner = dmx.Runner(weights, cfg, precision=dmx.PRECISION_BF16)
+    mix = dmx.signals.synthetic_mix(13, 1.0)
+    opts = dmx.SeparateOptions(shifts=1, overlap=0.25, batch_chunks=4)
+    ref = oracle.separate([model], mix[0], mix[1], 44100, opts)
+    out = dmx.separate_runners([runner], mix[0], mix[1], 44100, opts)
+    for s in range(4):
+        assert snr_db(ref[s], out[s]) >= 40.0, (s, snr_db(ref[s], out[s]))

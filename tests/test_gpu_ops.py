@@ -299,3 +299,77 @@ def test_ispec_sum_matches_oracle(lib, oracle, b, L):
     dxs, dxt, dn = dev(xs), dev(xt), dev(norms)
     call(lib, "dmx_op_ispec_sum", stream(), ptr(dxs), ptr(dxt), b, L, ptr(dn), ptr(out))
     assert snr_db(ref, out.cpu().numpy()) > 100
+
+
+# ---- bf16-MFMA variant: inputs rounded to bf16, fp32 accumulation and output.
+# Gate: rms-relative error <= 1e-2 against the fp32 oracle (bf16 keeps 8
+# mantissa bits, 2^-9 relative rounding per operand), and > 1e-5 so the test
+# proves the bf16 kernel ran rather than the fp32 one.
+
+@pytest.fixture
+def bf16(lib):
+    assert lib.dmx_op_set_precision(1) == 0
+    yield
+    assert lib.dmx_op_set_precision(0) == 0
+
+
+def test_bf16_precision_is_validated(lib):
+    assert lib.dmx_op_set_precision(7) != 0
+    assert lib.dmx_op_set_precision(0) == 0
+
+
+@pytest.mark.parametrize("rows,k,n,tail", [(300, 512, 1536, 0), (64, 512, 2048, 1), (129, 2048, 512, 2),
+                                           (37, 19, 70, 0)])
+def test_bf16_linear_matches_oracle(lib, oracle, bf16, rows, k, n, tail):
+    r = rng(rows + k + n + 1)
+    x = r.uniform(-0.4, 0.4, (rows, k)).astype(np.float32)
+    w = r.uniform(-0.4, 0.4, (n, k)).astype(np.float32)
+    b = r.uniform(-0.4, 0.4, n).astype(np.float32)
+    res = r.uniform(-1, 1, (rows, n)).astype(np.float32)
+    g = r.uniform(0.1, 0.5, n).astype(np.float32)
+    ref = oracle.sgemm(x, w.T) + b
+    if tail == 1:
+        ref = oracle.gelu(ref)
+    elif tail == 2:
+        ref = res + ref * g
+    dx, dw, db, dres, dg = dev(x), dev(w), dev(b), dev(res), dev(g)
+    out = torch.empty((rows, n), device="cuda")
+    call(lib, "dmx_op_linear", stream(), ptr(dx), rows, k, ptr(dw), ptr(db), n, tail, ptr(dres), ptr(dg), ptr(out))
+    err = rms_relative_error(ref, out.cpu().numpy())
+    assert 1e-5 < err < 1e-2, err
+
+
+@pytest.mark.parametrize("b,ic,h,w,C,kh,kw", [(1, 48, 32, 12, 48, 1, 1), (1, 16, 10, 9, 16, 3, 3),
+                                               (2, 24, 1, 300, 24, 1, 3)])
+def test_bf16_conv2d_glu_matches_oracle(lib, oracle, bf16, b, ic, h, w, C, kh, kw):
+    r = rng(C + kh + 1)
+    x = r.uniform(-0.4, 0.4, (b, ic, h, w)).astype(np.float32)
+    wt = r.uniform(-0.4, 0.4, (2 * C, ic, kh, kw)).astype(np.float32)
+    bias = r.uniform(-0.4, 0.4, 2 * C).astype(np.float32)
+    ref = oracle.glu(oracle.conv2d(x, wt, bias, (1, 1), (kh // 2, kw // 2)))
+    out = torch.empty(ref.shape, device="cuda")
+    dx, dwt, db = dev(x), dev(wt), dev(bias)
+    call(lib, "dmx_op_conv2d_glu", stream(), ptr(dx), None, b, ic, h, w, ptr(dwt), ptr(db), C, kh, kw, kh // 2,
+         kw // 2, None, ctypes.c_float(0.0), ptr(out))
+    err = rms_relative_error(ref, out.cpu().numpy())
+    assert 1e-5 < err < 1e-2, err
+
+
+@pytest.mark.parametrize("batch,heads,nq,nk", [(1, 8, 200, 130), (1, 1, 33, 1), (2, 8, 2688, 1344)])
+def test_bf16_attention_matches_oracle(lib, oracle, bf16, batch, heads, nq, nk):
+    r = rng(nq + nk + 1)
+    D = heads * 64
+    q = r.uniform(-2, 2, (batch, nq, D)).astype(np.float32)
+    k = r.uniform(-2, 2, (batch, nk, D)).astype(np.float32)
+    v = r.uniform(-2, 2, (batch, nk, D)).astype(np.float32)
+    ref = np.empty_like(q)
+    for bb in range(batch):
+        for h in range(heads):
+            sl = slice(64 * h, 64 * h + 64)
+            ref[bb, :, sl] = oracle.attention_head(q[bb, :, sl], k[bb, :, sl], v[bb, :, sl], 0.125)
+    out = torch.empty(q.shape, device="cuda")
+    dq, dk, dv = dev(q), dev(k), dev(v)
+    call(lib, "dmx_op_attention", stream(), ptr(dq), ptr(dk), ptr(dv), ptr(out), batch, heads, nq, nk,
+         ctypes.c_float(0.125))
+    err = rms_relative_error(ref, out.cpu().numpy())
+    assert (nk == 1 or 1e-5 < err) and err < 1e-2, err
