@@ -102,6 +102,118 @@ def copy_calibration(torch, mib: int = 256, iters: int = 5):
     return mib
 
 
+def transformer_flops(d=512, ff=2048, lf=2688, lt=1344, layers=5):
+    """Algorithmic FLOPs of the cross-transformer stack per batch element
+    (projections, QK^T and PV, FFN; 2 flops per MAC): self layers at even
+    indices, cross layers at odd ones, both branches."""
+    def self_layer(n):
+        return 2 * n * d * 3 * d + 4 * n * n * d + 2 * n * d * d + 4 * n * d * ff
+
+    def cross_layer(nq, nk):
+        return 2 * nq * d * d + 2 * nk * d * 2 * d + 4 * nq * nk * d + 2 * nq * d * d + 4 * nq * d * ff
+    total = 0
+    for i in range(layers):
+        total += (self_layer(lf) + self_layer(lt)) if i % 2 == 0 else (cross_layer(lf, lt) + cross_layer(lt, lf))
+    return float(total)
+
+
+def config2_transformer(pkg, torch, batch=8, iters=5):
+    """Config 2: the 5-layer cross-transformer alone on N(0, 1) activations,
+    2688 frequency tokens (8 x 336) and 1344 time tokens, Xavier-init."""
+    cfg = pkg.Config()
+    runner = pkg.Runner(pkg.xavier_transformer_init(0, cfg), cfg)
+    g = torch.Generator(device="cuda").manual_seed(0)
+    x = torch.randn((batch, 512, 8, 336), device="cuda", generator=g)
+    xt = torch.randn((batch, 512, 1344), device="cuda", generator=g)
+    ox, oxt = torch.empty_like(x), torch.empty_like(xt)
+    torch.cuda.synchronize()
+    run = lambda: runner.crosstransformer_device(x.data_ptr(), xt.data_ptr(), batch, 8, 336, 1344, ox.data_ptr(),
+                                                 oxt.data_ptr())
+    run()
+    runner.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(iters):
+        run()
+    runner.synchronize()
+    ms = 1000.0 * (time.perf_counter() - t0) / iters
+    flops = transformer_flops() * batch
+    return {"batch": batch, "ms": round(ms, 3), "tflops": round(flops / (ms * 1e-3) / 1e12, 2),
+            "flops_per_call": flops, "dtype": "f32"}
+
+
+def config4_bag(pkg, torch, seconds=180.0, batch_chunks=8):
+    """Config 4: four random-init networks (seeds 1-4), identity bag, shifts=1,
+    180 s synthetic mix resident in HBM; then StemSelection::Some([vocals])."""
+    cfg = pkg.Config()
+    runners = [pkg.Runner(pkg.random_init(seed, cfg), cfg) for seed in (1, 2, 3, 4)]
+    mix = pkg.signals.synthetic_mix(0, seconds)
+    samples = mix.shape[1]
+    d_mix = torch.from_numpy(mix).cuda()
+    d_stems = torch.empty((cfg.sources, 2, samples), device="cuda")
+    bag = np.eye(4, cfg.sources, dtype=np.float32)
+    opts = pkg.SeparateOptions(shifts=1, overlap=0.25, batch_chunks=batch_chunks).to_c()
+    lib = pkg._native.load()
+    handles = (ctypes.c_void_p * 4)(*[r.handle for r in runners])
+
+    def sep(wanted):
+        mask = None if wanted is None else (ctypes.c_uint8 * 4)(*wanted)
+        rc = lib.dmx_separate_device(handles, bag.ctypes.data_as(ctypes.POINTER(ctypes.c_float)), 4, mask,
+                                     ctypes.c_void_p(d_mix.data_ptr()), samples, cfg.samplerate, ctypes.byref(opts),
+                                     pkg._native.PROGRESS(), None, ctypes.c_void_p(d_stems.data_ptr()))
+        if rc != 0:
+            raise RuntimeError(pkg._native.last_error())
+        runners[0].synchronize()
+        torch.cuda.synchronize()
+
+    out = {}
+    for name, wanted in (("all_stems", None), ("vocals_only", (0, 0, 0, 1))):
+        sep(wanted)
+        t0 = time.perf_counter()
+        sep(wanted)
+        s = time.perf_counter() - t0
+        out[name] = {"x_realtime": round(seconds / s, 2), "ms": round(1000.0 * s, 2)}
+    out["workload"] = (f"{seconds:g} s mix, 4 networks (seeds 1-4), identity bag, shifts=1, overlap 0.25, "
+                       f"{batch_chunks} chunks per launch, fp32, mix and stems resident in HBM")
+    return out
+
+
+def config5_bf16(pkg, torch, batch=32, iters=3, check=2):
+    """Config 5: the full forward with bf16-MFMA contractions on 32 segments of
+    N(0, 0.1^2) noise (seed-7 weights); per-stem SNR of `check` of them against
+    the fp32 oracle on the host."""
+    cfg = pkg.Config()
+    w = pkg.random_init(7, cfg)
+    runner = pkg.Runner(w, cfg, precision=pkg.PRECISION_BF16)
+    L = cfg.training_length
+    mix = pkg.signals.gaussian_segments(7, batch, L)
+    d_mix = torch.from_numpy(mix).cuda()
+    d_out = torch.empty((batch, cfg.sources, 2, L), device="cuda")
+    lib = pkg._native.load()
+
+    def fwd():
+        rc = lib.dmx_forward_device(runner.handle, ctypes.c_void_p(d_mix.data_ptr()), batch, 2, L,
+                                    ctypes.c_void_p(d_out.data_ptr()))
+        if rc != 0:
+            raise RuntimeError(pkg._native.last_error())
+    fwd()
+    runner.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(iters):
+        fwd()
+    runner.synchronize()
+    s = (time.perf_counter() - t0) / iters
+    sys.path.insert(0, str(ROOT))
+    from oracle import binding as oracle
+    ref = oracle.Model(w, cfg).forward(mix[:check])
+    got = d_out[:check].cpu().numpy()
+    snr = min(10.0 * np.log10(np.sum(ref[:, s_].astype(np.float64) ** 2) /
+                              max(np.sum((ref[:, s_].astype(np.float64) - got[:, s_]) ** 2), 1e-30))
+              for s_ in range(cfg.sources))
+    return {"batch": batch, "ms": round(1000.0 * s, 2), "x_realtime": round(batch * L / cfg.samplerate / s, 2),
+            "min_stem_snr_db_vs_fp32_oracle": round(float(snr), 2), "snr_checked_segments": check,
+            "dtype": "bf16 MFMA inputs, f32 accumulate/softmax/norms/output"}
+
+
 def cpu_baseline(pkg, seconds_budget: float = 20.0):
     """The restated reference CPU backend on one 7.8 s segment (config 1):
     1 warm-up, then the median of up to 3 timed forwards within the budget."""
@@ -137,6 +249,8 @@ def main():
     ap.add_argument("--attn-iters", type=int, default=20)
     ap.add_argument("--roofline-only", action="store_true",
                     help="only the roofline kernel loop and the copy calibration (for rocprofv3 runs)")
+    ap.add_argument("--no-other-configs", action="store_true",
+                    help="skip the config 2 / 4 / 5 measurements reported beside the headline")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py: this build runs on one GPU only; multi-GPU runs are not part of it "
@@ -227,6 +341,11 @@ def main():
         "roofline": roofline,
         "cpu_baseline": None if args.no_cpu_baseline else cpu_baseline(pkg),
     }
+    if not args.no_other_configs:
+        del runner
+        line["other_configs"] = {"config2_transformer": config2_transformer(pkg, torch),
+                                 "config4_bag": config4_bag(pkg, torch),
+                                 "config5_bf16": config5_bf16(pkg, torch)}
     print(json.dumps(line))
 
 
