@@ -20,6 +20,7 @@ namespace {
 template <int KH, int KW>
 struct ConvGather {
     static constexpr bool kmajor = false;
+    __device__ bool fast() const { return true; }
     const float *x, *skip;
     int64_t outer, inner, cs;  // batch strides and channel stride
     int zdiv, h, w, kh_rt, kw_rt, sh, sw, ph, pw, dh, dw, ow;
@@ -52,6 +53,7 @@ struct ConvGather {
 // loading. y is (rows, H, T); stats holds (sum, sum_sq) per row.
 struct NormGeluRows {
     static constexpr bool kmajor = false;
+    __device__ bool fast() const { return true; }
     const float *y;
     const double *stats;
     const float *nw, *nb;
@@ -78,6 +80,7 @@ struct NormGeluRows {
 template <int TAPS>
 struct ConvTGather {
     static constexpr bool kmajor = false;
+    __device__ bool fast() const { return true; }
     const float *x;
     int ic, A, P, st, crop;
     struct State {
@@ -108,6 +111,8 @@ struct PhaseWeights {
         const float *row;
     };
     __device__ State setup(int z, int m) const { return {w + ((int64_t)(z % st) * oc + m) * K}; }
+    __device__ bool fast() const { return vec; }
+    __device__ float4 load4_full(const State &s, int k) const { return *reinterpret_cast<const float4 *>(s.row + k); }
     __device__ float4 load4(const State &s, int k, int Kt) const {
         if (vec && k + 3 < Kt) return *reinterpret_cast<const float4 *>(s.row + k);
         float4 v;
@@ -132,6 +137,8 @@ struct TokenGather {
         int f = n / T, t = n - f * T;
         return {tok + ((int64_t)z * F * T + (int64_t)t * F + f) * D};
     }
+    __device__ bool fast() const { return true; }  // the launcher requires D % 4 == 0 and aligned rows
+    __device__ float4 load4_full(const State &s, int k) const { return *reinterpret_cast<const float4 *>(s.row + k); }
     __device__ float4 load4(const State &s, int k, int K) const {
         if (k + 3 < K) return *reinterpret_cast<const float4 *>(s.row + k);
         float4 v;

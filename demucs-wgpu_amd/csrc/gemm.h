@@ -40,6 +40,11 @@ typedef float floatx16 __attribute__((ext_vector_type(16)));
 typedef float floatx4 __attribute__((ext_vector_type(4)));
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 
+// LLVM AMDGPU scheduling strategy for the k-loop (iglp_opt).
+#ifndef DMX_GEMM_IGLP
+#define DMX_GEMM_IGLP 1
+#endif
+
 // k-tile depth of the fp32 kernel (the bf16 kernel stages 32).
 #ifndef DMX_GEMM_BK
 #define DMX_GEMM_BK 16
@@ -113,46 +118,65 @@ __global__ __launch_bounds__(GEMM_THREADS) void gemm_kernel(int M, int N, int K,
     auto b_row = [&](int e) { return BL::kmajor ? e / KQ : e % BN; };
     auto b_quad = [&](int e) { return BL::kmajor ? e % KQ : e / BN; };
 
+    // Rows of A beyond M and columns of B beyond N only feed outputs the
+    // epilogue discards, so they read row / column 0 instead of being masked;
+    // only k >= K must read as zero, which matters in the last k-tile alone.
     typename AL::State ast[A_ITEMS];
     typename BL::State bst[B_ITEMS];
-    bool aok[A_ITEMS], bok[B_ITEMS];
 #pragma unroll
     for (int it = 0; it < A_ITEMS; ++it) {
         int e = tid + it * GEMM_THREADS;
         int pr = e < BM * KQ ? phys_row(a_row(e)) : -1;
-        aok[it] = pr >= 0;
-        ast[it] = al.setup(z, aok[it] ? pr : 0);
+        ast[it] = al.setup(z, pr >= 0 ? pr : 0);
     }
 #pragma unroll
     for (int it = 0; it < B_ITEMS; ++it) {
         int e = tid + it * GEMM_THREADS;
         int n = n0 + b_row(e);
-        bok[it] = e < BN * KQ && n < N;
-        bst[it] = bl.setup(z, bok[it] ? n : 0);
+        bst[it] = bl.setup(z, (e < BN * KQ && n < N) ? n : 0);
     }
 
     float4 areg[A_ITEMS], breg[B_ITEMS];
-    auto fetch = [&](const auto &ld, const auto &st, bool ok, int k) -> float4 {
+    // FULL: the whole k-tile lies below K and the sources allow unchecked
+    // vector loads, so no per-element test is compiled into the loads.
+    auto fetch = [&](const auto &ld, const auto &st, int k, auto full_tag) -> float4 {
         using L = std::decay_t<decltype(ld)>;
-        if (!ok) return make_float4(0.f, 0.f, 0.f, 0.f);
+        constexpr bool FULL = decltype(full_tag)::value;
         if constexpr (L::kmajor) {
-            return ld.load4(st, k, K);
+            if constexpr (FULL)
+                return ld.load4_full(st, k);
+            else
+                return ld.load4(st, k, K);
         } else {
             float4 v;
-            v.x = k < K ? ld.load(st, k) : 0.f;
-            v.y = k + 1 < K ? ld.load(st, k + 1) : 0.f;
-            v.z = k + 2 < K ? ld.load(st, k + 2) : 0.f;
-            v.w = k + 3 < K ? ld.load(st, k + 3) : 0.f;
+            if constexpr (FULL) {
+                v.x = ld.load(st, k);
+                v.y = ld.load(st, k + 1);
+                v.z = ld.load(st, k + 2);
+                v.w = ld.load(st, k + 3);
+            } else {
+                v.x = k < K ? ld.load(st, k) : 0.f;
+                v.y = k + 1 < K ? ld.load(st, k + 1) : 0.f;
+                v.z = k + 2 < K ? ld.load(st, k + 2) : 0.f;
+                v.w = k + 3 < K ? ld.load(st, k + 3) : 0.f;
+            }
             return v;
         }
     };
-    auto load_tiles = [&](int k0) {
+    auto load_tiles = [&](int k0, auto full_tag) {
 #pragma unroll
         for (int it = 0; it < A_ITEMS; ++it)
-            areg[it] = fetch(al, ast[it], aok[it], k0 + 4 * a_quad(tid + it * GEMM_THREADS));
+            areg[it] = fetch(al, ast[it], k0 + 4 * a_quad(tid + it * GEMM_THREADS), full_tag);
 #pragma unroll
         for (int it = 0; it < B_ITEMS; ++it)
-            breg[it] = fetch(bl, bst[it], bok[it], k0 + 4 * b_quad(tid + it * GEMM_THREADS));
+            breg[it] = fetch(bl, bst[it], k0 + 4 * b_quad(tid + it * GEMM_THREADS), full_tag);
+    };
+    const bool fast = al.fast() && bl.fast();
+    auto load_next = [&](int k0) {
+        if (fast && k0 + BK <= K)
+            load_tiles(k0, std::true_type{});
+        else
+            load_tiles(k0, std::false_type{});
     };
     auto put = [&](T *dst, const float4 &v) {
         if constexpr (BF16)
@@ -182,13 +206,16 @@ __global__ __launch_bounds__(GEMM_THREADS) void gemm_kernel(int M, int N, int K,
             for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
 
     const int nk = (K + BK - 1) / BK;
-    load_tiles(0);
+    load_next(0);
     store_tiles(0);
     __syncthreads();
     const int row_in = lane & 31, khalf = lane >> 5;
     for (int kt = 0; kt < nk; ++kt) {
         const int cur = kt & 1;
-        if (kt + 1 < nk) load_tiles((kt + 1) * BK);
+        if (kt + 1 < nk) load_next((kt + 1) * BK);
+#ifdef DMX_GEMM_SETPRIO  // tuning builds only
+        __builtin_amdgcn_s_setprio(1);
+#endif
         if constexpr (BF16) {
             // Lane half h holds k = 16g + 8h .. +7 of its row for A and B alike.
 #pragma unroll
@@ -225,6 +252,12 @@ __global__ __launch_bounds__(GEMM_THREADS) void gemm_kernel(int M, int N, int K,
                             acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[i][t], b[j][t], acc[i][j], 0, 0, 0);
             }
         }
+#ifdef DMX_GEMM_SETPRIO
+        __builtin_amdgcn_s_setprio(0);
+#endif
+        // Interleave the MFMAs with the LDS reads and the next tile's global
+        // loads (measured 2-20 % faster across the model's shapes).
+        __builtin_amdgcn_iglp_opt(DMX_GEMM_IGLP);
         if (kt + 1 < nk) store_tiles(cur ^ 1);
         __syncthreads();
     }
@@ -277,6 +310,8 @@ struct KMajor {
         const float *row;
     };
     __device__ State setup(int z, int row) const { return {p + z * batch_stride + (int64_t)row * ld}; }
+    __device__ bool fast() const { return vec; }
+    __device__ float4 load4_full(const State &s, int k) const { return *reinterpret_cast<const float4 *>(s.row + k); }
     __device__ float4 load4(const State &s, int k, int K) const {
         if (vec && k + 3 < K) return *reinterpret_cast<const float4 *>(s.row + k);
         float4 v;
@@ -297,6 +332,7 @@ struct MNMajor {
         const float *col;
     };
     __device__ State setup(int z, int mn) const { return {p + z * batch_stride + mn}; }
+    __device__ bool fast() const { return true; }
     __device__ float load(const State &s, int k) const { return s.col[(int64_t)k * ld]; }
 };
 
