@@ -76,7 +76,8 @@ int dmx_op_dconv_layer(void *stream, float *x, int B, int C, int F, int T, int d
                        const float *b2, const float *n2w, const float *n2b, const float *gamma) {
     return guarded([&] {
         hipStream_t s = as_stream(stream);
-        Scratch h((size_t)B * F * hidden * T * sizeof(float)), st((size_t)4 * B * F * sizeof(double));
+        Scratch h((size_t)dconv_hidden_floats(B * F, hidden, T) * sizeof(float)),
+            st((size_t)4 * B * F * sizeof(double));
         dconv_layer(s, x, B, C, F, T, dilation, w1, b1, hidden, n1w, n1b, w2, b2, n2w, n2b, gamma,
                     static_cast<float *>(h.p), static_cast<double *>(st.p));
         DMX_HIP(hipStreamSynchronize(s));

@@ -1,192 +1,366 @@
-// dconv.hip — the DConv residual layer for narrow branches (hidden = C/8 <= 12),
-// as three direct VALU passes with one thread per time position.
+// dconv.hip — the DConv residual layer for narrow branches (C = 48 or 96,
+// hidden H = C/8 = 6 or 12).
 //
 // Semantics: `dconv_forward` + `dconv_tail_into`
 // (crates/demucs-core/src/demucs/host.rs:985-1059, demucs/ops.rs:930-1094):
 //   y = conv1d_k3_dil(x) + b1;      GN(1, H) over (H, T) per row; GELU
 //   z = W2 . gelu(GN(y)) + b2;      GN(1, 2C) over (2C, T) per row
 //   x += gamma * (GN(z)[c] * sigmoid(GN(z)[C + c]))
-// With H <= 12 a 32-row MFMA tile would be >60% padding, and each pass is
-// bound by one sweep over x; these kernels do the useful FMAs only. The rows
-// are the (b, f) rows of a (B, C, F, T) tensor, addressed in place.
-//   pass 1: conv1 -> y (rows, H, T), GN1 statistics
-//   pass 2: GN1+GELU (on load) -> W2 -> GN2 statistics only
-//   pass 3: GN1+GELU -> W2 -> GN2 -> GLU -> LayerScale -> += into x
-// Recomputing W2 in pass 3 (2C*H FMAs per position) is cheaper than writing
-// and re-reading the 2C-channel intermediate.
+// The rows are the (b, f) rows of a (B, C, F, T) tensor, addressed in place.
+//
+// With H <= 12 a matrix-core tile would be mostly padding, so the two
+// contractions run on the VALU, one thread per position, 64 positions per
+// wave. Every weight and per-row coefficient is indexed uniformly across the
+// wave, so it is a scalar load and an SGPR operand: one VALU instruction per
+// FMA, no LDS traffic. Launches:
+//   0. W1 (H, C, 3) -> (C, 3, H), so each channel's 3H weights are contiguous.
+//   1. y = conv1(x) + b1, plus partial moments of y per 64 positions.
+//   2. per row: GN1 moments in f64 -> GN1 as an affine (scale, shift) per h.
+//   3. g = GELU(GN1(y)); per wave (up to 256 positions) the sums
+//      S_h = sum_t g_h and the Gram matrix G_hh' = sum_t g_h g_h' (h <= h').
+//   4. per row: those partials in f64, and GN2's moments from them, since
+//      z_o = W2[o] . g + b2[o] gives
+//        sum_t z_o   = W2[o] . S + T b2[o]
+//        sum_t z_o^2 = W2[o] G W2[o]^T + 2 b2[o] (W2[o] . S) + T b2[o]^2;
+//      GN2 (with b2 folded in) as an affine per channel o.
+//   5. z = W2 g, GN2, GLU, LayerScale, += into x.
+// x crosses HBM three times (two reads, one write); the 2C-channel z is never
+// stored and never formed for its statistics. Row reductions go through
+// partials, not same-address atomics (those serialise on the long time rows).
+// Loads read a clamped index unconditionally and are multiplied by a 0/1 mask
+// (a select lets the compiler turn each load into a branch); the data is
+// finite, so the product is exactly the zero padding.
 #include "common.h"
 #include "ops.h"
 
 namespace dmx {
 namespace {
 
-constexpr int DC_THREADS = 256;
-constexpr int DC_MAX_C = 96;
+constexpr int DC_THREADS = 256;  // 4 waves, one work item each
+constexpr int C1_POS = 64;       // positions per conv1 / apply work item
+constexpr int GR_ITER = 4;       // 64-position chunks per Gram work item
+constexpr float DC_LOG2E = 1.4426950408889634f;
 
-__device__ __forceinline__ const float *row_base(const float *x, int z, int C, int F, int T) {
+template <int H>
+constexpr int gram_terms() {
+    return H + H * (H + 1) / 2;
+}
+
+// Scratch layout inside `hbuf` (floats).
+struct NarrowScratch {
+    float *y, *part1, *aff1, *part, *aff2, *w1t;
+};
+template <int C, int H>
+NarrowScratch carve(float *hbuf, int rows, int T) {
+    NarrowScratch s;
+    const int64_t items64 = (int64_t)rows * ceil_div(T, C1_POS);
+    const int64_t items_g = (int64_t)rows * ceil_div(T, C1_POS * GR_ITER);
+    s.y = hbuf;
+    s.part1 = s.y + (int64_t)rows * H * T;
+    s.aff1 = s.part1 + 2 * items64;
+    s.part = s.aff1 + (int64_t)rows * H * 2;
+    s.aff2 = s.part + items_g * gram_terms<H>();
+    s.w1t = s.aff2 + (int64_t)rows * 2 * C * 2;
+    return s;
+}
+
+__device__ __forceinline__ int uniform(int v) { return __builtin_amdgcn_readfirstlane(v); }
+
+__device__ __forceinline__ float *row_ptr(float *x, int z, int C, int F, int T) {
     int b = z / F, f = z - b * F;
     return x + ((int64_t)b * C * F + f) * T;
 }
 
-template <int H>
-__global__ __launch_bounds__(DC_THREADS) void dconv_conv1_kernel(const float *__restrict__ x, int C, int F, int T,
-                                                                 int dil, const float *__restrict__ w1,
+__device__ __forceinline__ float fast_sigmoid(float v) {
+    return __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-v * DC_LOG2E));
+}
+
+__global__ void dconv_w1_transpose_kernel(const float *__restrict__ w1, int C, int H, float *__restrict__ w1t) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;  // i = (h * C + c) * 3 + k
+    if (i >= H * C * 3) return;
+    const int h = i / (C * 3), ck = i - h * C * 3;
+    w1t[ck * H + h] = w1[i];
+}
+
+// 1. y = conv1(x) + b1; per-item (sum, sum of squares) of y.
+template <int C, int H>
+__global__ __launch_bounds__(DC_THREADS) void dconv_conv1_kernel(const float *__restrict__ x, int F, int T, int dil,
+                                                                 int items_per_row, int n_items,
+                                                                 const float *__restrict__ w1t,
                                                                  const float *__restrict__ b1, float *__restrict__ y,
-                                                                 double *__restrict__ stats) {
-    __shared__ float ws[H * DC_MAX_C * 3];
-    const int z = blockIdx.y;
-    for (int i = threadIdx.x; i < H * C * 3; i += DC_THREADS) ws[i] = w1[i];
-    __syncthreads();
-    const int t = blockIdx.x * DC_THREADS + threadIdx.x;
-    const bool ok = t < T;
-    const float *xr = row_base(x, z, C, F, T);
+                                                                 float *__restrict__ part1) {
+    const int lane = threadIdx.x & 63;
+    const int item = uniform(blockIdx.x * 4 + (threadIdx.x >> 6));
+    if (item >= n_items) return;
+    const int z = uniform(item / items_per_row);
+    const int t = (item - z * items_per_row) * C1_POS + lane;
+    const float *xr = row_ptr(const_cast<float *>(x), z, C, F, T);
     const int64_t cs = (int64_t)F * T;
+    const int tl = t - dil, tr = t + dil;
+    const int il = min(max(tl, 0), T - 1), ic = min(t, T - 1), ir = min(tr, T - 1);
+    const float ml = tl >= 0 && tl < T ? 1.0f : 0.0f, mc = t < T ? 1.0f : 0.0f, mr = tr < T ? 1.0f : 0.0f;
     float acc[H];
 #pragma unroll
-    for (int h = 0; h < H; ++h) acc[h] = 0.0f;
-    if (ok) {
-        const bool l_ok = t - dil >= 0, r_ok = t + dil < T;
-        for (int c = 0; c < C; ++c) {
-            const float *xc = xr + c * cs;
-            float x0 = l_ok ? xc[t - dil] : 0.0f, x1 = xc[t], x2 = r_ok ? xc[t + dil] : 0.0f;
+    for (int h = 0; h < H; ++h) acc[h] = b1[h];
+#pragma unroll 4
+    for (int c = 0; c < C; ++c) {
+        const float *xc = xr + c * cs;
+        const float x0 = xc[il] * ml, x1 = xc[ic] * mc, x2 = xc[ir] * mr;
+        const float *w = w1t + c * 3 * H;
 #pragma unroll
-            for (int h = 0; h < H; ++h) {
-                const float *w = ws + (h * C + c) * 3;
-                acc[h] += w[0] * x0 + w[1] * x1 + w[2] * x2;
-            }
-        }
+        for (int h = 0; h < H; ++h) acc[h] = fmaf(w[h], x0, fmaf(w[H + h], x1, fmaf(w[2 * H + h], x2, acc[h])));
     }
-    double s = 0.0, q = 0.0;
-    if (ok) {
+    float fs = 0.0f, fq = 0.0f;
+    if (t < T) {
         float *yr = y + (int64_t)z * H * T + t;
 #pragma unroll
         for (int h = 0; h < H; ++h) {
-            float v = acc[h] + b1[h];
-            yr[(int64_t)h * T] = v;
-            s += v;
-            q += (double)v * v;
+            yr[(int64_t)h * T] = acc[h];
+            fs += acc[h];
+            fq += acc[h] * acc[h];
         }
     }
-    block_moments_atomic(s, q, stats + 2 * z);
-}
-
-// GN1 + GELU of this position's H conv1 outputs.
-template <int H>
-__device__ __forceinline__ void load_hidden(const float *y, int z, int T, int t, const double *stats1,
-                                            const float *n1w, const float *n1b, float g[H]) {
-    float mean, inv;
-    gn_stats(stats1 + 2 * z, (double)H * T, mean, inv);
-    const float *yr = y + (int64_t)z * H * T + t;
-#pragma unroll
-    for (int h = 0; h < H; ++h) {
-        float scale = inv * n1w[h];
-        float shift = n1b[h] - mean * scale;
-        g[h] = gelu(yr[(int64_t)h * T] * scale + shift);
+    fs = wave_sum(fs);
+    fq = wave_sum(fq);
+    if (lane == 0) {
+        part1[2 * item] = fs;
+        part1[2 * item + 1] = fq;
     }
 }
 
-template <int H>
-__global__ __launch_bounds__(DC_THREADS) void dconv_conv2_stats_kernel(const float *__restrict__ y, int C, int T,
-                                                                       const double *__restrict__ stats1,
-                                                                       const float *__restrict__ n1w,
-                                                                       const float *__restrict__ n1b,
-                                                                       const float *__restrict__ w2,
-                                                                       const float *__restrict__ b2,
-                                                                       double *__restrict__ stats2) {
-    __shared__ float ws[2 * DC_MAX_C * H];
-    __shared__ float bs[2 * DC_MAX_C];
-    const int z = blockIdx.y;
-    for (int i = threadIdx.x; i < 2 * C * H; i += DC_THREADS) ws[i] = w2[i];
-    for (int i = threadIdx.x; i < 2 * C; i += DC_THREADS) bs[i] = b2[i];
+// One block sums the NS-term partials of row z in f64 into `out` (LDS): the
+// block's threads split into 256 / NS groups, thread (j, i) sums term i over
+// items j, j + groups, ..., then one thread per term adds the groups.
+template <int NS>
+__device__ void sum_row_partials(const float *part, int items_per_row, int z, double *out) {
+    static_assert(NS <= DC_THREADS, "one thread per term at least");
+    constexpr int GROUPS = DC_THREADS / NS;
+    __shared__ double red[GROUPS * NS];
+    const int i = threadIdx.x % NS, j = threadIdx.x / NS;
+    const float *p = part + (int64_t)z * items_per_row * NS + i;
+    if (j < GROUPS) {
+        double a = 0.0;
+        for (int it = j; it < items_per_row; it += GROUPS) a += (double)p[(int64_t)it * NS];
+        red[j * NS + i] = a;
+    }
     __syncthreads();
-    const int t = blockIdx.x * DC_THREADS + threadIdx.x;
-    double s = 0.0, q = 0.0;
-    if (t < T) {
+    if (threadIdx.x < NS) {
+        double a = 0.0;
+        for (int g = 0; g < GROUPS; ++g) a += red[g * NS + threadIdx.x];
+        out[threadIdx.x] = a;
+    }
+    __syncthreads();
+}
+
+// 2. GN1 of row z as (scale, shift) per hidden channel.
+__global__ __launch_bounds__(DC_THREADS) void dconv_gn1_kernel(const float *__restrict__ part1, int items_per_row,
+                                                               int H, int T, const float *__restrict__ n1w,
+                                                               const float *__restrict__ n1b,
+                                                               float *__restrict__ aff1) {
+    __shared__ double sums[2];
+    const int z = blockIdx.x;
+    sum_row_partials<2>(part1, items_per_row, z, sums);
+    if (threadIdx.x < H) {
+        float mean, inv;
+        gn_stats(sums, (double)H * T, mean, inv);
+        const int h = threadIdx.x;
+        const float scale = inv * n1w[h];
+        aff1[(z * H + h) * 2] = scale;
+        aff1[(z * H + h) * 2 + 1] = n1b[h] - mean * scale;
+    }
+}
+
+// GN1 + GELU of the H hidden channels at position t (clamped; masked by m).
+template <int H>
+__device__ __forceinline__ void hidden(const float *y, int z, int T, int t, float m, const float *aff1, float g[H]) {
+    const float *yr = y + (int64_t)z * H * T + min(t, T - 1);
+    const float *a = aff1 + z * H * 2;
+#pragma unroll
+    for (int h = 0; h < H; ++h) g[h] = gelu(yr[(int64_t)h * T] * a[2 * h] + a[2 * h + 1]) * m;
+}
+
+// 3. Per wave (GR_ITER chunks of 64 positions): S_h and the upper triangle of
+// G, accumulated per lane, then wave-reduced.
+template <int H>
+__global__ __launch_bounds__(DC_THREADS) void dconv_gram_kernel(const float *__restrict__ y, int T, int items_per_row,
+                                                                int n_items, const float *__restrict__ aff1,
+                                                                float *__restrict__ part) {
+    constexpr int NS = gram_terms<H>();
+    const int lane = threadIdx.x & 63;
+    const int item = uniform(blockIdx.x * 4 + (threadIdx.x >> 6));
+    if (item >= n_items) return;
+    const int z = uniform(item / items_per_row);
+    const int t_begin = (item - z * items_per_row) * (C1_POS * GR_ITER);
+    float acc[NS];
+#pragma unroll
+    for (int i = 0; i < NS; ++i) acc[i] = 0.0f;
+    for (int c = 0; c < GR_ITER; ++c) {
+        if (t_begin + c * C1_POS >= T) break;  // uniform
+        const int t = t_begin + c * C1_POS + lane;
         float g[H];
-        load_hidden<H>(y, z, T, t, stats1, n1w, n1b, g);
-        for (int o = 0; o < 2 * C; ++o) {
-            float v = 0.0f;
+        hidden<H>(y, z, T, t, t < T ? 1.0f : 0.0f, aff1, g);
+        int i = 0;
 #pragma unroll
-            for (int h = 0; h < H; ++h) v += ws[o * H + h] * g[h];
-            v += bs[o];
-            s += v;
-            q += (double)v * v;
-        }
+        for (int h = 0; h < H; ++h, ++i) acc[i] += g[h];
+#pragma unroll
+        for (int h = 0; h < H; ++h)
+#pragma unroll
+            for (int h2 = h; h2 < H; ++h2, ++i) acc[i] = fmaf(g[h], g[h2], acc[i]);
     }
-    block_moments_atomic(s, q, stats2 + 2 * z);
+    float *out = part + (int64_t)item * NS;
+#pragma unroll
+    for (int i = 0; i < NS; ++i) {
+        const float v = wave_sum(acc[i]);
+        if (lane == 0) out[i] = v;
+    }
 }
 
-template <int H>
-__global__ __launch_bounds__(DC_THREADS) void dconv_apply_kernel(float *__restrict__ x, const float *__restrict__ y,
-                                                                 int C, int F, int T, const double *__restrict__ stats1,
-                                                                 const float *__restrict__ n1w,
-                                                                 const float *__restrict__ n1b,
-                                                                 const float *__restrict__ w2,
-                                                                 const float *__restrict__ b2,
-                                                                 const double *__restrict__ stats2,
-                                                                 const float *__restrict__ n2w,
-                                                                 const float *__restrict__ n2b,
-                                                                 const float *__restrict__ gamma) {
-    __shared__ float ws[2 * DC_MAX_C * H];
-    __shared__ float bs[2 * DC_MAX_C], sc[2 * DC_MAX_C], sh[2 * DC_MAX_C], gm[DC_MAX_C];
-    const int z = blockIdx.y;
-    float mean2, inv2;
-    gn_stats(stats2 + 2 * z, 2.0 * C * (double)T, mean2, inv2);
-    for (int i = threadIdx.x; i < 2 * C * H; i += DC_THREADS) ws[i] = w2[i];
-    for (int i = threadIdx.x; i < 2 * C; i += DC_THREADS) {
-        bs[i] = b2[i];
-        float scale = inv2 * n2w[i];
-        sc[i] = scale;
-        sh[i] = n2b[i] - mean2 * scale;
+// 4. One block per row: S and G in f64, GN2's moments, GN2 as (scale, shift)
+// per channel o with b2 folded into the shift.
+template <int C, int H>
+__global__ __launch_bounds__(DC_THREADS) void dconv_gn2_kernel(const float *__restrict__ part, int items_per_row,
+                                                               int T, const float *__restrict__ w2,
+                                                               const float *__restrict__ b2,
+                                                               const float *__restrict__ n2w,
+                                                               const float *__restrict__ n2b,
+                                                               float *__restrict__ aff2) {
+    constexpr int NS = gram_terms<H>();
+    __shared__ double sg[NS];
+    __shared__ double red[2][DC_THREADS / 64];
+    __shared__ double mom[2];
+    const int z = blockIdx.x;
+    sum_row_partials<NS>(part, items_per_row, z, sg);
+    auto gram = [&](int h, int h2) -> double {  // G[h][h2] from the stored upper triangle
+        if (h > h2) {
+            const int t = h;
+            h = h2;
+            h2 = t;
+        }
+        return sg[H + h * H - h * (h - 1) / 2 + (h2 - h)];
+    };
+    double sz = 0.0, sz2 = 0.0;
+    for (int o = threadIdx.x; o < 2 * C; o += DC_THREADS) {
+        const float *w = w2 + (int64_t)o * H;
+        double ws = 0.0, quad = 0.0;
+        for (int h = 0; h < H; ++h) {
+            ws += (double)w[h] * sg[h];
+            double inner = 0.0;
+            for (int h2 = 0; h2 < H; ++h2) inner += (double)w[h2] * gram(h, h2);
+            quad += (double)w[h] * inner;
+        }
+        const double b = b2[o];
+        sz += ws + (double)T * b;
+        sz2 += quad + 2.0 * b * ws + (double)T * b * b;
     }
-    for (int i = threadIdx.x; i < C; i += DC_THREADS) gm[i] = gamma[i];
+    sz = wave_sum_d(sz);
+    sz2 = wave_sum_d(sz2);
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    if (lane == 0) {
+        red[0][wave] = sz;
+        red[1][wave] = sz2;
+    }
     __syncthreads();
-    const int t = blockIdx.x * DC_THREADS + threadIdx.x;
-    if (t >= T) return;
+    if (threadIdx.x == 0) {
+        double a = 0.0, b = 0.0;
+        for (int w = 0; w < DC_THREADS / 64; ++w) {
+            a += red[0][w];
+            b += red[1][w];
+        }
+        mom[0] = a;
+        mom[1] = b;
+    }
+    __syncthreads();
+    float mean, inv;
+    gn_stats(mom, 2.0 * C * (double)T, mean, inv);
+    for (int o = threadIdx.x; o < 2 * C; o += DC_THREADS) {
+        const float scale = inv * n2w[o];
+        aff2[(z * 2 * C + o) * 2] = scale;
+        aff2[(z * 2 * C + o) * 2 + 1] = n2b[o] + (b2[o] - mean) * scale;
+    }
+}
+
+// 5. z = W2 g per position, GN2, GLU, LayerScale, += into x.
+template <int C, int H>
+__global__ __launch_bounds__(DC_THREADS) void dconv_apply_kernel(float *__restrict__ x, const float *__restrict__ y,
+                                                                 int F, int T, int items_per_row, int n_items,
+                                                                 const float *__restrict__ aff1,
+                                                                 const float *__restrict__ w2,
+                                                                 const float *__restrict__ aff2,
+                                                                 const float *__restrict__ gamma) {
+    const int lane = threadIdx.x & 63;
+    const int item = uniform(blockIdx.x * 4 + (threadIdx.x >> 6));
+    if (item >= n_items) return;
+    const int z = uniform(item / items_per_row);
+    const int t = (item - z * items_per_row) * C1_POS + lane;
     float g[H];
-    load_hidden<H>(y, z, T, t, stats1, n1w, n1b, g);
-    float *xr = const_cast<float *>(row_base(x, z, C, F, T)) + t;
+    hidden<H>(y, z, T, t, 1.0f, aff1, g);
+    if (t >= T) return;
+    float *xr = row_ptr(x, z, C, F, T) + t;
     const int64_t cs = (int64_t)F * T;
+    const float *a2 = aff2 + z * 2 * C * 2;
+#pragma unroll 4
     for (int c = 0; c < C; ++c) {
+        const float *wv = w2 + c * H, *wg = w2 + (C + c) * H;
         float v = 0.0f, u = 0.0f;
 #pragma unroll
         for (int h = 0; h < H; ++h) {
-            v += ws[c * H + h] * g[h];
-            u += ws[(C + c) * H + h] * g[h];
+            v = fmaf(wv[h], g[h], v);
+            u = fmaf(wg[h], g[h], u);
         }
-        float value = (v + bs[c]) * sc[c] + sh[c];
-        float gate = (u + bs[C + c]) * sc[C + c] + sh[C + c];
-        xr[c * cs] += gm[c] * (value * sigmoid(gate));
+        const float value = fmaf(v, a2[2 * c], a2[2 * c + 1]);
+        const float gate = fmaf(u, a2[2 * (C + c)], a2[2 * (C + c) + 1]);
+        xr[c * cs] = fmaf(gamma[c], value * fast_sigmoid(gate), xr[c * cs]);
     }
 }
 
-template <int H>
-void launch_all(hipStream_t s, float *x, int B, int C, int F, int T, int dil, const float *w1, const float *b1,
+template <int C, int H>
+void launch_all(hipStream_t s, float *x, int B, int F, int T, int dil, const float *w1, const float *b1,
                 const float *n1w, const float *n1b, const float *w2, const float *b2, const float *n2w,
-                const float *n2b, const float *gamma, float *hbuf, double *stats) {
+                const float *n2b, const float *gamma, float *hbuf) {
     const int rows = B * F;
-    double *st1 = stats, *st2 = stats + 2 * rows;
-    dim3 grid((unsigned)ceil_div(T, DC_THREADS), (unsigned)rows);
-    hipLaunchKernelGGL(dconv_conv1_kernel<H>, grid, dim3(DC_THREADS), 0, s, x, C, F, T, dil, w1, b1, hbuf, st1);
+    const NarrowScratch sc = carve<C, H>(hbuf, rows, T);
+    const int per_row64 = ceil_div(T, C1_POS), per_row_g = ceil_div(T, C1_POS * GR_ITER);
+    const int items64 = rows * per_row64, items_g = rows * per_row_g;
+    hipLaunchKernelGGL(dconv_w1_transpose_kernel, dim3((unsigned)ceil_div(H * C * 3, 256)), dim3(256), 0, s, w1, C, H,
+                       sc.w1t);
     DMX_LAUNCH_CHECK();
-    hipLaunchKernelGGL(dconv_conv2_stats_kernel<H>, grid, dim3(DC_THREADS), 0, s, hbuf, C, T, st1, n1w, n1b, w2, b2,
-                       st2);
+    hipLaunchKernelGGL((dconv_conv1_kernel<C, H>), dim3((unsigned)ceil_div(items64, 4)), dim3(DC_THREADS), 0, s, x, F,
+                       T, dil, per_row64, items64, sc.w1t, b1, sc.y, sc.part1);
     DMX_LAUNCH_CHECK();
-    hipLaunchKernelGGL(dconv_apply_kernel<H>, grid, dim3(DC_THREADS), 0, s, x, hbuf, C, F, T, st1, n1w, n1b, w2, b2,
-                       st2, n2w, n2b, gamma);
+    hipLaunchKernelGGL(dconv_gn1_kernel, dim3((unsigned)rows), dim3(DC_THREADS), 0, s, sc.part1, per_row64, H, T, n1w,
+                       n1b, sc.aff1);
+    DMX_LAUNCH_CHECK();
+    hipLaunchKernelGGL(dconv_gram_kernel<H>, dim3((unsigned)ceil_div(items_g, 4)), dim3(DC_THREADS), 0, s, sc.y, T,
+                       per_row_g, items_g, sc.aff1, sc.part);
+    DMX_LAUNCH_CHECK();
+    hipLaunchKernelGGL((dconv_gn2_kernel<C, H>), dim3((unsigned)rows), dim3(DC_THREADS), 0, s, sc.part, per_row_g, T,
+                       w2, b2, n2w, n2b, sc.aff2);
+    DMX_LAUNCH_CHECK();
+    hipLaunchKernelGGL((dconv_apply_kernel<C, H>), dim3((unsigned)ceil_div(items64, 4)), dim3(DC_THREADS), 0, s, x,
+                       sc.y, F, T, per_row64, items64, sc.aff1, w2, sc.aff2, gamma);
     DMX_LAUNCH_CHECK();
 }
 
 }  // namespace
 
+int64_t dconv_hidden_floats(int rows, int H, int T) {
+    // y, conv1 partials, GN1 affine, Gram partials, GN2 affine, transposed W1
+    // (the narrow path's layout; the wide path uses y alone).
+    const int C = 8 * H;
+    const int64_t items64 = (int64_t)rows * ceil_div(T, C1_POS);
+    const int64_t items_g = (int64_t)rows * ceil_div(T, C1_POS * GR_ITER);
+    return (int64_t)rows * H * T + 2 * items64 + (int64_t)rows * H * 2 + items_g * (H + H * (H + 1) / 2) +
+           (int64_t)rows * 2 * C * 2 + (int64_t)C * 3 * H;
+}
+
 bool dconv_layer_narrow(hipStream_t s, float *x, int B, int C, int F, int T, int dil, const float *w1,
                         const float *b1, int H, const float *n1w, const float *n1b, const float *w2, const float *b2,
                         const float *n2w, const float *n2b, const float *gamma, float *hbuf, double *stats) {
-    if (C > DC_MAX_C || B * F > 65535) return false;
+    (void)stats;
     if (H == 6 && C == 48)
-        launch_all<6>(s, x, B, C, F, T, dil, w1, b1, n1w, n1b, w2, b2, n2w, n2b, gamma, hbuf, stats);
+        launch_all<48, 6>(s, x, B, F, T, dil, w1, b1, n1w, n1b, w2, b2, n2w, n2b, gamma, hbuf);
     else if (H == 12 && C == 96)
-        launch_all<12>(s, x, B, C, F, T, dil, w1, b1, n1w, n1b, w2, b2, n2w, n2b, gamma, hbuf, stats);
+        launch_all<96, 12>(s, x, B, F, T, dil, w1, b1, n1w, n1b, w2, b2, n2w, n2b, gamma, hbuf);
     else
         return false;
     return true;

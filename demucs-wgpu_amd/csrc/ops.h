@@ -51,6 +51,8 @@ void dconv_layer(hipStream_t s, float *x, int B, int C, int F, int T, int dil, c
 
 // The same layer with direct VALU kernels for hidden widths where MFMA tiles
 // would be mostly padding (dconv.hip); returns false when it does not apply.
+// Floats of the hidden-activation scratch `hbuf` that dconv_layer needs.
+int64_t dconv_hidden_floats(int rows, int H, int T);
 bool dconv_layer_narrow(hipStream_t s, float *x, int B, int C, int F, int T, int dil, const float *w1,
                         const float *b1, int H, const float *n1w, const float *n1b, const float *w2, const float *b2,
                         const float *n2w, const float *n2b, const float *gamma, float *hbuf, double *stats);

@@ -296,7 +296,7 @@ void run_dconv(dmx_runner &r, hipStream_t s, float *x, int B, int C, int F, int 
     const int rows = B * F;
     for (int d = 0; d < 2; ++d) {
         const DConvW &D = L.dconv[d];
-        DBuf h = fbuf(s, (int64_t)rows * D.hidden * T);
+        DBuf h = fbuf(s, dconv_hidden_floats(rows, D.hidden, T));
         DBuf st = dbuf(s, 4 * (int64_t)rows);
         dconv_layer(s, x, B, C, F, T, 1 << d, D.w1, D.b1, D.hidden, D.n1w, D.n1b, D.w2, D.b2, D.n2w, D.n2b, D.gamma,
                     h.f(), st.d());
