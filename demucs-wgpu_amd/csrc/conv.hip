@@ -275,11 +275,24 @@ struct EpLinear {
 // Tile selection
 // ---------------------------------------------------------------------------
 
+// Column tile of the 48-channel GLU shapes.
+#ifndef DMX_GLU96_BN
+#define DMX_GLU96_BN 64
+#endif
+#ifndef DMX_GLU48_BN
+#define DMX_GLU48_BN 128
+#endif
+
 template <bool GLU, bool BF16, class AL, class BL, class EP>
 void gemm_pick(hipStream_t s, int M, int N, int K, int batches, const AL &al, const BL &bl, const EP &ep) {
     if constexpr (GLU) {
-        if (M > 32)
-            launch_gemm<128, 128, 2, true, BF16>(s, M, N, K, batches, al, bl, ep);
+        // M = C output channels; a block covers BM / 2 of them.
+        if (M % 96 == 0)
+            launch_gemm<192, DMX_GLU96_BN, 2, true, BF16>(s, M, N, K, batches, al, bl, ep);  // 2 x 48 channels
+        else if (M == 48)
+            launch_gemm<96, DMX_GLU48_BN, 1, true, BF16>(s, M, N, K, batches, al, bl, ep);   // 1 x 48 channels
+        else if (M > 32)
+            launch_gemm<128, 128, 2, true, BF16>(s, M, N, K, batches, al, bl, ep);  // 2 x 32 channels
         else
             launch_gemm<64, 128, 1, true, BF16>(s, M, N, K, batches, al, bl, ep);
     } else {
@@ -288,7 +301,11 @@ void gemm_pick(hipStream_t s, int M, int N, int K, int batches, const AL &al, co
             launch_gemm<DMX_BIG_BM, DMX_BIG_BN, DMX_BIG_WM, false, BF16>(s, M, N, K, batches, al, bl, ep);
         else
 #endif
-        if (M >= 96)
+        if (M % 96 == 0 && M >= 192 && M <= 768)  // channel counts 192, 384, 768: 96-row wave tiles
+            launch_gemm<192, 64, 2, false, BF16>(s, M, N, K, batches, al, bl, ep);
+        else if (M == 96)
+            launch_gemm<96, 128, 1, false, BF16>(s, M, N, K, batches, al, bl, ep);
+        else if (M >= 96)
             launch_gemm<128, 128, 2, false, BF16>(s, M, N, K, batches, al, bl, ep);
         else if (M > 32)
             launch_gemm<64, 128, 2, false, BF16>(s, M, N, K, batches, al, bl, ep);

@@ -25,9 +25,12 @@
 // MFMAs. k-major sources are read as float4 along k; m/n-major sources are
 // read four k at a time per column (coalesced across lanes along m/n).
 //
-// GLU mode: each wave's two 32-row m-tiles hold the value channels c and the
-// gate channels C + c of the same outputs, so GLU happens in registers and the
-// 2C-channel product is never written.
+// GLU mode: each wave's m-tiles hold WTM/2 value channels c followed by the
+// gate channels C + c of the same outputs (two tiles = 32 channels, or three
+// tiles = 48 channels, which fits C = 48 and 96 without padding). A value
+// row's gate row is WTM/2 rows further on, which is a multiple of 8, so it
+// lies in the same lane: GLU happens in registers and the 2C-channel product
+// is never written.
 #pragma once
 
 #include <type_traits>
@@ -85,7 +88,8 @@ __global__ __launch_bounds__(GEMM_THREADS) void gemm_kernel(int M, int N, int K,
     constexpr int WTM = BM / WAVES_M, WTN = BN / WAVES_N;
     constexpr int TM = WTM / 32, TN = WTN / 32;
     static_assert(TM >= 1 && TN >= 1, "wave tile must hold at least one 32x32 MFMA tile");
-    static_assert(!GLU || TM == 2, "GLU needs exactly one value and one gate tile per wave");
+    static_assert(!GLU || TM == 2 || TM == 3, "GLU waves hold 32 or 48 channels (value + gate tiles)");
+    constexpr int GCH = WTM / 2;  // GLU channels per wave
     __shared__ __align__(16) T As[2][BM][LD];
     __shared__ __align__(16) T Bs[2][BN][LD];
 
@@ -99,10 +103,11 @@ __global__ __launch_bounds__(GEMM_THREADS) void gemm_kernel(int M, int N, int K,
     // Logical tile row -> physical A row (-1 when out of range).
     auto phys_row = [&](int lr) -> int {
         if constexpr (GLU) {
-            int w = lr / WTM, t = (lr % WTM) / 32, i = lr % 32;
-            int c = m_block + w * 32 + i;
+            const int w = lr / WTM, i = lr % WTM;
+            const bool gate = i >= GCH;
+            const int c = m_block + w * GCH + (gate ? i - GCH : i);
             if (c >= M) return -1;
-            return t ? M + c : c;
+            return gate ? M + c : c;
         } else {
             int r = m_block + lr;
             return r < M ? r : -1;
@@ -270,8 +275,16 @@ __global__ __launch_bounds__(GEMM_THREADS) void gemm_kernel(int M, int N, int K,
         for (int r = 0; r < 16; ++r) {
             const int rr = 8 * (r / 4) + 4 * khalf + (r % 4);
             if constexpr (GLU) {
-                const int c = m_block + wm * 32 + rr;
-                if (c < M && n < N) ep.glu(z, c, n, acc[0][j][r], acc[1][j][r]);
+                // 8-row block b = 32 i + 8 (r / 4) of the wave tile; its gate
+                // block b + GCH is tile gi, register gr of this same lane.
+#pragma unroll
+                for (int i = 0; i < TM; ++i) {
+                    const int b = 32 * i + 8 * (r / 4);
+                    if (b >= GCH) continue;
+                    const int gi = (b + GCH) / 32, gr = (((b + GCH) % 32) / 8) * 4 + r % 4;
+                    const int c = m_block + wm * GCH + 32 * i + rr;
+                    if (c < M && n < N) ep.glu(z, c, n, acc[i][j][r], acc[gi][j][gr]);
+                }
             } else {
 #pragma unroll
                 for (int i = 0; i < TM; ++i) {
