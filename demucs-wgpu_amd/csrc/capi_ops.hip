@@ -2,6 +2,7 @@
 // caller's stream, for the parity tests.
 #include <hip/hip_runtime.h>
 
+#include <memory>
 #include <vector>
 
 #include "../../include/dmx_ops.h"
@@ -32,6 +33,23 @@ struct Scratch {
     ~Scratch() { (void)hipFree(p); }
 };
 
+// A device conv weight (oc, ic, kh, kw) in GEMM order (conv_gemm_weights):
+// the weight itself when that is its PyTorch layout, else a repacked copy
+// held by `keep` (the caller synchronises before `keep` goes).
+const float *gemm_weights(hipStream_t s, const float *w, int oc, int ic, int kh, int kw,
+                          std::unique_ptr<Scratch> &keep) {
+    if (!conv_tap_major(ic, kh, kw)) return w;
+    require_ptrs({w}, "conv weight");
+    const size_t n = (size_t)oc * ic * kh * kw;
+    std::vector<float> h(n), g(n);
+    DMX_HIP(hipStreamSynchronize(s));
+    DMX_HIP(hipMemcpy(h.data(), w, n * sizeof(float), hipMemcpyDeviceToHost));
+    conv_gemm_weights(h.data(), oc, ic, kh, kw, g.data());
+    keep = std::make_unique<Scratch>(n * sizeof(float));
+    DMX_HIP(hipMemcpy(keep->p, g.data(), n * sizeof(float), hipMemcpyHostToDevice));
+    return static_cast<const float *>(keep->p);
+}
+
 }  // namespace
 
 extern "C" {
@@ -40,8 +58,11 @@ int dmx_op_conv2d(void *stream, const float *x, const float *skip, int b, int ic
                   const float *bias, int oc, int kh, int kw, int sh, int sw, int ph, int pw, int dh, int dw, int act,
                   float *out) {
     return guarded([&] {
-        conv2d(as_stream(stream), x, skip, b, ic, h, w, weight, bias, oc, kh, kw, sh, sw, ph, pw, dh, dw, out,
-               (Act)act);
+        hipStream_t s = as_stream(stream);
+        std::unique_ptr<Scratch> keep;
+        const float *wg = gemm_weights(s, weight, oc, ic, kh, kw, keep);
+        conv2d(s, x, skip, b, ic, h, w, wg, bias, oc, kh, kw, sh, sw, ph, pw, dh, dw, out, (Act)act);
+        if (keep) DMX_HIP(hipStreamSynchronize(s));
     });
 }
 
@@ -49,7 +70,11 @@ int dmx_op_conv2d_glu(void *stream, const float *x, const float *skip, int b, in
                       const float *weight, const float *bias, int C, int kh, int kw, int ph, int pw, const float *emb,
                       float emb_scale, float *out) {
     return guarded([&] {
-        conv2d_glu(as_stream(stream), x, skip, b, ic, h, w, weight, bias, C, kh, kw, ph, pw, out, emb, emb_scale);
+        hipStream_t s = as_stream(stream);
+        std::unique_ptr<Scratch> keep;
+        const float *wg = gemm_weights(s, weight, 2 * C, ic, kh, kw, keep);
+        conv2d_glu(s, x, skip, b, ic, h, w, wg, bias, C, kh, kw, ph, pw, out, emb, emb_scale);
+        if (keep) DMX_HIP(hipStreamSynchronize(s));
     });
 }
 
@@ -78,7 +103,9 @@ int dmx_op_dconv_layer(void *stream, float *x, int B, int C, int F, int T, int d
         hipStream_t s = as_stream(stream);
         Scratch h((size_t)dconv_hidden_floats(B * F, hidden, T) * sizeof(float)),
             st((size_t)4 * B * F * sizeof(double));
-        dconv_layer(s, x, B, C, F, T, dilation, w1, b1, hidden, n1w, n1b, w2, b2, n2w, n2b, gamma,
+        std::unique_ptr<Scratch> keep;
+        const float *w1g = gemm_weights(s, w1, hidden, C, 1, 3, keep);
+        dconv_layer(s, x, B, C, F, T, dilation, w1, w1g, b1, hidden, n1w, n1b, w2, b2, n2w, n2b, gamma,
                     static_cast<float *>(h.p), static_cast<double *>(st.p));
         DMX_HIP(hipStreamSynchronize(s));
     });

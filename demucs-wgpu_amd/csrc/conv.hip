@@ -49,6 +49,57 @@ struct ConvGather {
     }
 };
 
+// The same gather in channel-quad order: k = (c / 4 * taps + tap) * 4 + c % 4,
+// matching weights in GEMM order (conv_tap_major). The four k of a quad are
+// four channels at one tap: one bounds test, then four loads one channel
+// stride apart; the taps of a quad are adjacent in k, so the input rows of
+// one k-tile are mostly the previous tile's (cache hits). SKIP adds the skip
+// tensor in finish(), after the k-tile's MFMAs.
+template <int KH, int KW, bool SKIP>
+struct ConvGatherTM {
+    static constexpr bool kmajor = false;
+    __device__ bool fast() const { return true; }
+    const float *x, *skip;
+    int64_t outer, inner, cs;  // batch strides and channel stride
+    int zdiv, h, w, sh, sw, ph, pw, dh, dw, ow, kh_rt, kw_rt;
+    using State = typename ConvGather<KH, KW>::State;
+    struct Raw {
+        float4 x, s;
+    };
+    __device__ int kw() const { return KW > 0 ? KW : kw_rt; }
+    __device__ int taps() const { return KH > 0 && KW > 0 ? KH * KW : kh_rt * kw_rt; }
+    __device__ State setup(int z, int n) const {
+        int oy = n / ow, ox = n - oy * ow;
+        int64_t off = (int64_t)(z / zdiv) * outer + (int64_t)(z % zdiv) * inner;
+        return {x + off, SKIP ? skip + off : nullptr, oy * sh - ph, ox * sw - pw};
+    }
+    __device__ Raw zero_raw() const {
+        const float4 z = make_float4(0.f, 0.f, 0.f, 0.f);
+        return {z, z};
+    }
+    __device__ Raw load_raw(const State &s, int k) const {
+        const int q = k >> 2, cq = q / taps(), tap = q - cq * taps();
+        const int ky = tap / kw(), kx = tap - ky * kw();
+        const int iy = s.iy0 + ky * dh, ix = s.ix0 + kx * dw;
+        if (iy < 0 || iy >= h || ix < 0 || ix >= w) return zero_raw();
+        const int64_t at = 4 * cq * cs + (int64_t)iy * w + ix;
+        const float *p = s.base + at;
+        Raw r;
+        r.x = make_float4(p[0], p[cs], p[2 * cs], p[3 * cs]);
+        if constexpr (SKIP) {
+            const float *q2 = s.sbase + at;
+            r.s = make_float4(q2[0], q2[cs], q2[2 * cs], q2[3 * cs]);
+        }
+        return r;
+    }
+    __device__ float4 finish(const State &, const Raw &r, int) const {
+        if constexpr (SKIP)
+            return make_float4(r.x.x + r.s.x, r.x.y + r.s.y, r.x.z + r.s.z, r.x.w + r.s.w);
+        else
+            return r.x;
+    }
+};
+
 // DConv conv2's input: GroupNorm(1) + GELU of conv1's output, applied while
 // loading. y is (rows, H, T); stats holds (sum, sum_sq) per row.
 struct NormGeluRows {
@@ -71,6 +122,38 @@ struct NormGeluRows {
         float scale = s.inv * nw[k];
         float shift = nb[k] - s.mean * scale;
         return gelu(s.col[(int64_t)k * T] * scale + shift);
+    }
+};
+
+// NormGeluRows for H % 4 == 0, split in two: load_raw fetches four hidden
+// rows of the column before the k-tile's MFMAs, finish applies GN + GELU
+// after them (k >= H finishes to zero).
+struct NormGeluQuads {
+    static constexpr bool kmajor = false;
+    __device__ bool fast() const { return true; }
+    const float *y;
+    const double *stats;
+    const float *nw, *nb;
+    int H, T;
+    using State = NormGeluRows::State;
+    using Raw = float4;
+    __device__ State setup(int z, int n) const {
+        float mean, inv;
+        gn_stats(stats + 2 * z, (double)H * (double)T, mean, inv);
+        return {y + (int64_t)z * H * T + n, mean, inv};
+    }
+    __device__ Raw zero_raw() const { return make_float4(0.f, 0.f, 0.f, 0.f); }
+    __device__ Raw load_raw(const State &s, int k) const {
+        const float *p = s.col + (int64_t)k * T;
+        return make_float4(p[0], p[T], p[2 * (int64_t)T], p[3 * (int64_t)T]);
+    }
+    __device__ float4 finish(const State &s, const Raw &r, int k) const {
+        if (k >= H) return make_float4(0.f, 0.f, 0.f, 0.f);
+        auto one = [&](float v, int kk) {
+            const float scale = s.inv * nw[kk];
+            return gelu(v * scale + (nb[kk] - s.mean * scale));
+        };
+        return make_float4(one(r.x, k), one(r.y, k + 1), one(r.z, k + 2), one(r.w, k + 3));
     }
 };
 
@@ -266,6 +349,58 @@ struct EpLinear {
         }
         out[at] = a;
     }
+    // A wave's TM x TN fragments of a tile that lies wholly in range:
+    // fragment (i, j) register r is row mb + 32 i + 8 (r / 4) + 4 khalf + r % 4,
+    // column nb + 32 j + col. The residual rows are all loaded before the
+    // first is used, so the loads overlap instead of each waiting in turn.
+    template <int TM, int TN>
+    __device__ void store_frags(int z, int mb, int nb, int col, int khalf, const floatx16 (&v)[TM][TN]) {
+        float *o = out + z * batch_stride;
+        const float *res = residual ? residual + z * batch_stride : nullptr;
+        auto at = [&](int i, int j, int r) -> int64_t {
+            return (int64_t)(mb + 32 * i + 8 * (r / 4) + 4 * khalf + r % 4) * ldo + nb + 32 * j + col;
+        };
+        if (tail == TAIL_RESIDUAL_SCALE) {
+            // One fragment row (TN x 16 residuals) in flight at a time keeps
+            // the register count at the main loop's.
+#pragma unroll
+            for (int i = 0; i < TM; ++i) {
+                float rv[TN][16];
+#pragma unroll
+                for (int j = 0; j < TN; ++j)
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) rv[j][r] = res[at(i, j, r)];
+#pragma unroll
+                for (int j = 0; j < TN; ++j) {
+                    const float bn = bias[nb + 32 * j + col], gn = gamma[nb + 32 * j + col];
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) {
+                        const float a = rv[j][r] + (v[i][j][r] + bn) * gn;
+                        if (stats) acc.add(a);
+                        o[at(i, j, r)] = a;
+                    }
+                }
+            }
+        } else if (tail == TAIL_BIAS_GELU) {
+#pragma unroll
+            for (int j = 0; j < TN; ++j) {
+                const float bn = bias[nb + 32 * j + col];
+#pragma unroll
+                for (int i = 0; i < TM; ++i)
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) o[at(i, j, r)] = gelu(v[i][j][r] + bn);
+            }
+        } else {
+#pragma unroll
+            for (int j = 0; j < TN; ++j) {
+                const float bn = bias[nb + 32 * j + col];
+#pragma unroll
+                for (int i = 0; i < TM; ++i)
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) o[at(i, j, r)] = v[i][j][r] + bn;
+            }
+        }
+    }
     __device__ void finalize(int z) {
         if (stats) acc.flush(stats + 2 * z);
     }
@@ -274,6 +409,11 @@ struct EpLinear {
 // ---------------------------------------------------------------------------
 // Tile selection
 // ---------------------------------------------------------------------------
+
+// k-tiles in flight in the direct-to-LDS linear kernel (0 = use gemm_kernel).
+#ifndef DMX_DMA_STAGES
+#define DMX_DMA_STAGES 3
+#endif
 
 // Column tile of the 48-channel GLU shapes.
 #ifndef DMX_GLU96_BN
@@ -354,12 +494,69 @@ ConvGather<KH, KW> gather(const float *x, const float *skip, int64_t outer, int6
     return g;
 }
 
+template <int KH, int KW, bool SKIP>
+ConvGatherTM<KH, KW, SKIP> gather_tm(const float *x, const float *skip, int64_t outer, int64_t inner, int zdiv,
+                                     int ic_stride_h, int h, int w, int sh, int sw, int ph, int pw, int dh, int dw,
+                                     int ow, int kh, int kw) {
+    ConvGatherTM<KH, KW, SKIP> g;
+    g.kh_rt = kh;
+    g.kw_rt = kw;
+    g.x = x;
+    g.skip = skip;
+    g.outer = outer;
+    g.inner = inner;
+    g.cs = (int64_t)ic_stride_h * w;
+    g.zdiv = zdiv;
+    g.h = h;
+    g.w = w;
+    g.sh = sh;
+    g.sw = sw;
+    g.ph = ph;
+    g.pw = pw;
+    g.dh = dh;
+    g.dw = dw;
+    g.ow = ow;
+    return g;
+}
+
 // Runs a conv GEMM with a compile-time kernel when it is one of the model's.
+// K = ic * kh * kw; the weight rows are in GEMM order (tap-major when
+// conv_tap_major(ic, kh, kw)).
 template <bool GLU, class EP>
 void conv_dispatch(hipStream_t s, int M, int N, int K, int batches, const KMajor &wa, const float *x,
                    const float *skip, int64_t outer, int64_t inner, int zdiv, int ic_stride_h, int h, int w, int kh,
                    int kw, int sh, int sw, int ph, int pw, int dh, int dw, int ow, const EP &ep) {
     require_ptrs({x, wa.p}, "conv");
+    const int ic = K / (kh * kw);
+    DMX_REQUIRE(ic * kh * kw == K, "conv: K is not ic * kh * kw");
+    if (conv_tap_major(ic, kh, kw)) {
+#define DMX_CONV_TM_CASE(A, B, S)                                                                          \
+    if (kh == A && kw == B && (skip != nullptr) == S) {                                                      \
+        gemm_auto<GLU>(s, M, N, K, batches, wa,                                                              \
+                       gather_tm<A, B, S>(x, skip, outer, inner, zdiv, ic_stride_h, h, w, sh, sw, ph, pw, dh,  \
+                                          dw, ow, kh, kw),                                                   \
+                       ep);                                                                                  \
+        return;                                                                                              \
+    }
+        // Encoders and DConv gather without a skip; decoder rewrites with one.
+        DMX_CONV_TM_CASE(8, 1, false)
+        DMX_CONV_TM_CASE(1, 8, false)
+        DMX_CONV_TM_CASE(3, 3, true)
+        DMX_CONV_TM_CASE(1, 3, true)
+        DMX_CONV_TM_CASE(1, 3, false)
+#undef DMX_CONV_TM_CASE
+        if (skip)
+            gemm_auto<GLU>(s, M, N, K, batches, wa,
+                           gather_tm<0, 0, true>(x, skip, outer, inner, zdiv, ic_stride_h, h, w, sh, sw, ph, pw, dh,
+                                                 dw, ow, kh, kw),
+                           ep);
+        else
+            gemm_auto<GLU>(s, M, N, K, batches, wa,
+                           gather_tm<0, 0, false>(x, skip, outer, inner, zdiv, ic_stride_h, h, w, sh, sw, ph, pw, dh,
+                                                  dw, ow, kh, kw),
+                           ep);
+        return;
+    }
 #define DMX_CONV_CASE(A, B)                                                                                \
     if (kh == A && kw == B) {                                                                                \
         gemm_auto<GLU>(s, M, N, K, batches, wa,                                                              \
@@ -437,6 +634,18 @@ void conv2d_glu(hipStream_t s, const float *x, const float *skip, int b, int ic,
                         ph, pw, 1, 1, ow, ep);
 }
 
+void conv_gemm_weights(const float *w, int oc, int ic, int kh, int kw, float *out) {
+    const int taps = kh * kw;
+    const bool tm = conv_tap_major(ic, kh, kw);
+    for (int o = 0; o < oc; ++o)
+        for (int c = 0; c < ic; ++c)
+            for (int t = 0; t < taps; ++t) {
+                const int64_t src = ((int64_t)o * ic + c) * taps + t;
+                const int64_t dst = tm ? (int64_t)o * ic * taps + ((int64_t)(c / 4) * taps + t) * 4 + c % 4 : src;
+                out[dst] = w[src];
+            }
+}
+
 int conv_transpose_taps(int k, int st) { return (k + st - 1) / st; }
 
 void pack_conv_transpose(const float *w, int ic, int oc, int k, int st, float *packed) {
@@ -477,10 +686,11 @@ void conv_transpose_axis(hipStream_t s, const float *x, int b, int ic, int A, in
     gemm_auto<false>(s, oc, N, K, b * st, pw, g, ep);
 }
 
-void dconv_layer(hipStream_t s, float *x, int B, int C, int F, int T, int dil, const float *w1, const float *b1,
-                 int H, const float *n1w, const float *n1b, const float *w2, const float *b2, const float *n2w,
-                 const float *n2b, const float *gamma, float *hbuf, double *stats) {
-    require_ptrs({x, w1, b1, n1w, n1b, w2, b2, n2w, n2b, gamma, hbuf, stats}, "dconv_layer");
+void dconv_layer(hipStream_t s, float *x, int B, int C, int F, int T, int dil, const float *w1,
+                 const float *w1_gemm, const float *b1, int H, const float *n1w, const float *n1b, const float *w2,
+                 const float *b2, const float *n2w, const float *n2b, const float *gamma, float *hbuf,
+                 double *stats) {
+    require_ptrs({x, w1, w1_gemm, b1, n1w, n1b, w2, b2, n2w, n2b, gamma, hbuf, stats}, "dconv_layer");
     const int rows = B * F;
     DMX_REQUIRE(rows <= 65535, "dconv_layer: too many rows for one launch");
     double *st1 = stats, *st2 = stats + 2 * rows;
@@ -493,14 +703,12 @@ void dconv_layer(hipStream_t s, float *x, int B, int C, int F, int T, int dil, c
     e1.stats = st1;
     e1.H = H;
     e1.T = T;
-    conv_dispatch<false>(s, H, T, C * 3, rows, kmajor(w1, C * 3, 0), x, nullptr, (int64_t)C * F * T, T, F, F, 1, T, 1, 3,
-                         1, 1, 0, dil, 1, dil, T, e1);
+    conv_dispatch<false>(s, H, T, C * 3, rows, kmajor(w1_gemm, C * 3, 0), x, nullptr, (int64_t)C * F * T, T, F, F, 1, T,
+                         1, 3, 1, 1, 0, dil, 1, dil, T, e1);
     // conv2 (1x1 over H) twice: statistics, then GN + GLU + LayerScale + residual.
-    NormGeluRows ng{hbuf, st1, n1w, n1b, H, T};
     EpConv2Stats e2;
     e2.bias = b2;
     e2.stats = st2;
-    gemm_auto<false>(s, 2 * C, T, H, rows, kmajor(w2, H, 0), ng, e2);
     EpConv2Apply e3;
     e3.x = x;
     e3.bias = b2;
@@ -511,7 +719,15 @@ void dconv_layer(hipStream_t s, float *x, int B, int C, int F, int T, int dil, c
     e3.C = C;
     e3.F = F;
     e3.T = T;
-    gemm_auto<true>(s, C, T, H, rows, kmajor(w2, H, 0), ng, e3);
+    if (H % 4 == 0) {
+        NormGeluQuads ng{hbuf, st1, n1w, n1b, H, T};
+        gemm_auto<false>(s, 2 * C, T, H, rows, kmajor(w2, H, 0), ng, e2);
+        gemm_auto<true>(s, C, T, H, rows, kmajor(w2, H, 0), ng, e3);
+    } else {
+        NormGeluRows ng{hbuf, st1, n1w, n1b, H, T};
+        gemm_auto<false>(s, 2 * C, T, H, rows, kmajor(w2, H, 0), ng, e2);
+        gemm_auto<true>(s, C, T, H, rows, kmajor(w2, H, 0), ng, e3);
+    }
 }
 
 void pointwise(hipStream_t s, const float *w, const float *bias, const float *x, int batches, int M, int K, int N,
@@ -540,6 +756,17 @@ void linear(hipStream_t s, const float *x, int64_t ldx, int64_t x_batch_stride, 
     ep.ldo = ldo;
     ep.batch_stride = out_batch_stride;
     ep.tail = tail;
+    const bool dma_ok = mfma_precision() == MfmaPrecision::FP32 && K % 16 == 0 && aligned16(x) && aligned16(w) &&
+                        ldx % 4 == 0 && x_batch_stride % 4 == 0;
+#if DMX_DMA_STAGES > 0
+    if (dma_ok) {
+        launch_gemm_dma<128, 128, 2, DMX_DMA_STAGES>(s, M, N, K, batches, KMajorRows{x, ldx, x_batch_stride},
+                                                     KMajorRows{w, K, 0}, ep);
+        return;
+    }
+#else
+    (void)dma_ok;
+#endif
     gemm_auto<false>(s, M, N, K, batches, kmajor(x, ldx, x_batch_stride), kmajor(w, K, 0), ep);
 }
 

@@ -77,6 +77,41 @@ struct GemmStage<true> {
     static constexpr int BK = 32;
 };
 
+// An m/n-major loader may fetch four consecutive k of one column at once
+// (load_quad, k a multiple of 4); when K is a multiple of 4 a quad is either
+// wholly below K or wholly past it.
+template <class L, class = void>
+struct has_load_quad : std::false_type {};
+template <class L>
+struct has_load_quad<L, std::void_t<decltype(&L::load_quad)>> : std::true_type {};
+
+// An m/n-major loader may also split a quad in two: load_raw(state, k)
+// only issues the loads (returning the loaded values as its Raw type) and
+// finish(state, raw, k) turns them into the operand (a skip add, a norm).
+// The kernel issues load_raw before a k-tile's MFMAs and calls finish after
+// them, just before the LDS store, so the loads are in flight during the
+// MFMAs instead of being waited for on the spot. zero_raw() finishes to 0.
+template <class L, class = void>
+struct has_load_raw : std::false_type {};
+template <class L>
+struct has_load_raw<L, std::void_t<typename L::Raw>> : std::true_type {};
+template <class L, bool = has_load_raw<L>::value>
+struct raw_of {
+    using type = float4;
+};
+template <class L>
+struct raw_of<L, true> {
+    using type = typename L::Raw;
+};
+
+// Row addressing of a k-major fp32 matrix for the direct-to-LDS kernel:
+// row r of problem z starts at p + z * batch_stride + r * ld.
+struct KMajorRows {
+    const float *p;
+    int64_t ld, batch_stride;
+    __device__ const float *row(int z, int r) const { return p + z * batch_stride + (int64_t)r * ld; }
+};
+
 template <int BM, int BN, int WAVES_M, bool GLU, bool BF16, class AL, class BL, class EP>
 __global__ __launch_bounds__(GEMM_THREADS) void gemm_kernel(int M, int N, int K, AL al, BL bl, EP ep) {
     using T = typename GemmStage<BF16>::T;
@@ -141,7 +176,9 @@ __global__ __launch_bounds__(GEMM_THREADS) void gemm_kernel(int M, int N, int K,
         bst[it] = bl.setup(z, (e < BN * KQ && n < N) ? n : 0);
     }
 
-    float4 areg[A_ITEMS], breg[B_ITEMS];
+    constexpr bool B_RAW = has_load_raw<BL>::value;
+    float4 areg[A_ITEMS];
+    typename raw_of<BL>::type breg[B_ITEMS];
     // FULL: the whole k-tile lies below K and the sources allow unchecked
     // vector loads, so no per-element test is compiled into the loads.
     auto fetch = [&](const auto &ld, const auto &st, int k, auto full_tag) -> float4 {
@@ -152,6 +189,9 @@ __global__ __launch_bounds__(GEMM_THREADS) void gemm_kernel(int M, int N, int K,
                 return ld.load4_full(st, k);
             else
                 return ld.load4(st, k, K);
+        } else if constexpr (has_load_quad<L>::value) {
+            if (FULL || k < K) return ld.load_quad(st, k);
+            return make_float4(0.f, 0.f, 0.f, 0.f);
         } else {
             float4 v;
             if constexpr (FULL) {
@@ -173,8 +213,13 @@ __global__ __launch_bounds__(GEMM_THREADS) void gemm_kernel(int M, int N, int K,
         for (int it = 0; it < A_ITEMS; ++it)
             areg[it] = fetch(al, ast[it], k0 + 4 * a_quad(tid + it * GEMM_THREADS), full_tag);
 #pragma unroll
-        for (int it = 0; it < B_ITEMS; ++it)
-            breg[it] = fetch(bl, bst[it], k0 + 4 * b_quad(tid + it * GEMM_THREADS), full_tag);
+        for (int it = 0; it < B_ITEMS; ++it) {
+            const int k = k0 + 4 * b_quad(tid + it * GEMM_THREADS);
+            if constexpr (B_RAW)
+                breg[it] = (decltype(full_tag)::value || k < K) ? bl.load_raw(bst[it], k) : bl.zero_raw();
+            else
+                breg[it] = fetch(bl, bst[it], k, full_tag);
+        }
     };
     const bool fast = al.fast() && bl.fast();
     auto load_next = [&](int k0) {
@@ -189,7 +234,7 @@ __global__ __launch_bounds__(GEMM_THREADS) void gemm_kernel(int M, int N, int K,
         else
             *reinterpret_cast<float4 *>(dst) = v;
     };
-    auto store_tiles = [&](int buf) {
+    auto store_tiles = [&](int buf, int k0) {
 #pragma unroll
         for (int it = 0; it < A_ITEMS; ++it) {
             int e = tid + it * GEMM_THREADS;
@@ -198,7 +243,12 @@ __global__ __launch_bounds__(GEMM_THREADS) void gemm_kernel(int M, int N, int K,
 #pragma unroll
         for (int it = 0; it < B_ITEMS; ++it) {
             int e = tid + it * GEMM_THREADS;
-            if (e < BN * KQ) put(&Bs[buf][b_row(e)][4 * b_quad(e)], breg[it]);
+            if (e < BN * KQ) {
+                if constexpr (B_RAW)
+                    put(&Bs[buf][b_row(e)][4 * b_quad(e)], bl.finish(bst[it], breg[it], k0 + 4 * b_quad(e)));
+                else
+                    put(&Bs[buf][b_row(e)][4 * b_quad(e)], breg[it]);
+            }
         }
     };
 
@@ -212,7 +262,7 @@ __global__ __launch_bounds__(GEMM_THREADS) void gemm_kernel(int M, int N, int K,
 
     const int nk = (K + BK - 1) / BK;
     load_next(0);
-    store_tiles(0);
+    store_tiles(0, 0);
     __syncthreads();
     const int row_in = lane & 31, khalf = lane >> 5;
     for (int kt = 0; kt < nk; ++kt) {
@@ -263,7 +313,7 @@ __global__ __launch_bounds__(GEMM_THREADS) void gemm_kernel(int M, int N, int K,
         // Interleave the MFMAs with the LDS reads and the next tile's global
         // loads (measured 2-20 % faster across the model's shapes).
         __builtin_amdgcn_iglp_opt(DMX_GEMM_IGLP);
-        if (kt + 1 < nk) store_tiles(cur ^ 1);
+        if (kt + 1 < nk) store_tiles(cur ^ 1, (kt + 1) * BK);
         __syncthreads();
     }
 
@@ -306,6 +356,214 @@ void launch_gemm(hipStream_t stream, int M, int N, int K, int batches, const AL 
     DMX_REQUIRE(grid.y <= 65535 && grid.z <= 65535, "GEMM grid too large");
     hipLaunchKernelGGL((gemm_kernel<BM, BN, WAVES_M, GLU, BF16, AL, BL, EP>), grid, dim3(GEMM_THREADS), 0, stream, M,
                        N, K, al, bl, ep);
+    DMX_LAUNCH_CHECK();
+}
+
+// ---------------------------------------------------------------------------
+// Direct-to-LDS GEMM for two k-major fp32 operands (the transformer linears:
+// activations (M, K) times weights (N, K)).
+//
+// The operand tiles go from global memory straight into LDS with
+// global_load_lds_dwordx4: no staging registers and no ds_write, so STAGES
+// k-tiles can be in flight at once while the MFMAs work on the oldest one.
+// One DMA instruction fills 1 KB of LDS, lane l writing bytes [16 l, 16 l + 16):
+// sixteen 64-byte rows (BK = 16 floats) of four 16-byte chunks. Lane l fetches
+// row l / 4 of its group and, in slot l % 4, the chunk (l % 4) ^ swz(row), so
+// a ds_read_b128 of one logical chunk over 16 consecutive rows touches 16
+// distinct bank quads (and 8 consecutive rows 8 distinct ones): the XOR
+// swizzle makes the MFMA operand reads conflict-free without padding, which a
+// DMA row layout cannot have.
+//
+// Waits: each wave counts its own DMA instructions with vmcnt (loads retire in
+// order); the barrier after the wait makes every wave's part of the k-tile
+// visible, and it also guarantees that the buffer refilled next was read by
+// every wave in the previous iteration. The operand reads are issued as
+// inline ds_read_b128 with explicit lgkmcnt waits: the compiler cannot tell
+// which stage a read touches, and would otherwise put a vmcnt(0) (wait for
+// every DMA in flight) in front of each of them, which serialises the
+// pipeline.
+// ---------------------------------------------------------------------------
+
+__device__ __forceinline__ int dma_swz(int r) { return ((r >> 1) ^ (r >> 3)) & 3; }
+
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
+// One DMA instruction: lane l copies 16 bytes from src to dst + 16 l bytes
+// (dst is wave-uniform). A plain __device__ function, so the device-only
+// builtin never sits in a lambda that the host side also analyses.
+__device__ __forceinline__ void dma_b128(const float *src, float *dst) {
+    __builtin_amdgcn_global_load_lds(src, dst, 16, 0, 0);
+}
+
+// 16 bytes from LDS (p points into a __shared__ array).
+__device__ __forceinline__ floatx4 lds_read_b128(const float *p) {
+    floatx4 v;
+    const unsigned addr = (unsigned)(uintptr_t)p;  // low 32 bits of a shared address = LDS offset
+    asm volatile("ds_read_b128 %0, %1" : "=v"(v) : "v"(addr) : "memory");
+    return v;
+}
+
+// Passes values through an empty volatile asm: no use of them can be
+// scheduled before the asm statements that precede this one.
+template <int TA, int TB>
+__device__ __forceinline__ void pin_regs(floatx4 (&a)[TA], floatx4 (&b)[TB]) {
+#pragma unroll
+    for (int i = 0; i < TA; ++i) asm volatile("" : "+v"(a[i]));
+#pragma unroll
+    for (int j = 0; j < TB; ++j) asm volatile("" : "+v"(b[j]));
+}
+
+// Waits for every LDS read in flight, then pins the values read.
+template <int TA, int TB>
+__device__ __forceinline__ void lds_wait(floatx4 (&a)[TA], floatx4 (&b)[TB]) {
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    pin_regs(a, b);
+}
+
+// Three waves per SIMD (three 4-wave blocks per CU, as the LDS of STAGES = 3
+// allows): registers are capped at 168, which the epilogue must fit too.
+template <int BM, int BN, int WAVES_M, int STAGES, class EP>
+__global__ __launch_bounds__(GEMM_THREADS) __attribute__((amdgpu_waves_per_eu(3))) void gemm_dma_kernel(int M, int N, int K, KMajorRows al, KMajorRows bl,
+                                                                EP ep) {
+    constexpr int BK = 16;                     // two MFMA k-groups of 8 per k-tile
+    constexpr int ROWS = BM + BN;              // staged rows per k-tile: A rows, then B rows
+    constexpr int INSTR = ROWS / 16;           // 1 KB DMA instructions per k-tile
+    constexpr int PER_WAVE = INSTR / 4;
+    constexpr int STAGE = ROWS * BK;           // floats per k-tile
+    static_assert(BM % 16 == 0 && BN % 16 == 0 && INSTR % 4 == 0, "tile rows must fill whole DMA instructions");
+    static_assert(STAGES >= 2 && PER_WAVE * (STAGES - 2) < 64, "pipeline depth");
+    constexpr int WAVES_N = 4 / WAVES_M;
+    constexpr int WTM = BM / WAVES_M, WTN = BN / WAVES_N;
+    constexpr int TM = WTM / 32, TN = WTN / 32;
+    static_assert(TM >= 1 && TN >= 1, "wave tile must hold at least one 32x32 MFMA tile");
+    __shared__ __align__(16) float lds[STAGES * STAGE];
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int wm = wave % WAVES_M, wn = wave / WAVES_M;
+    const int z = blockIdx.z;
+    const int n0 = blockIdx.x * BN, m0 = blockIdx.y * BM;
+    ep.init(z);
+
+    // Sources of this lane's DMA slots. Rows past M / N repeat the last row:
+    // they only feed outputs the epilogue discards.
+    const int grow = lane >> 2, gchunk = (lane & 3) ^ dma_swz(lane >> 2);
+    const float *src[PER_WAVE];
+#pragma unroll
+    for (int i = 0; i < PER_WAVE; ++i) {
+        const int r = 16 * (wave + 4 * i) + grow;
+        if (r < BM)
+            src[i] = al.row(z, min(m0 + r, M - 1)) + 4 * gchunk;
+        else
+            src[i] = bl.row(z, min(n0 + r - BM, N - 1)) + 4 * gchunk;
+    }
+    auto issue = [&](int buf, int k0) {
+#pragma unroll
+        for (int i = 0; i < PER_WAVE; ++i)
+            dma_b128(src[i] + k0, &lds[buf * STAGE + (wave + 4 * i) * 256]);
+    };
+
+    floatx16 acc[TM][TN];
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+
+    // LDS float offsets of this lane's operand rows (row * BK), and their swizzle.
+    const int row_in = lane & 31, khalf = lane >> 5;
+    int a_off[TM], a_swz[TM], b_off[TN], b_swz[TN];
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
+        const int r = wm * WTM + i * 32 + row_in;
+        a_off[i] = r * BK;
+        a_swz[i] = dma_swz(r & 15);
+    }
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+        const int r = BM + wn * WTN + j * 32 + row_in;
+        b_off[j] = r * BK;
+        b_swz[j] = dma_swz(r & 15);
+    }
+
+    const int nk = K / BK;
+#pragma unroll
+    for (int st = 0; st < STAGES - 1; ++st)
+        if (st < nk) issue(st, st * BK);
+    for (int kt = 0; kt < nk; ++kt) {
+        if (kt + STAGES - 2 < nk)
+            wait_vmcnt<PER_WAVE * (STAGES - 2)>();
+        else
+            wait_vmcnt<0>();
+        __builtin_amdgcn_s_barrier();
+        if (kt + STAGES - 1 < nk) issue((kt + STAGES - 1) % STAGES, (kt + STAGES - 1) * BK);
+        const float *stage = lds + (kt % STAGES) * STAGE;
+        // Group g holds k = 8g .. 8g + 7; lane half h reads its logical chunk
+        // 2g + h (k = 8g + 4h .. +3). Group 1's reads fly during group 0's MFMAs.
+        floatx4 a[2][TM], b[2][TN];
+        auto read_group = [&](int g) {
+            const int c = 2 * g + khalf;
+#pragma unroll
+            for (int i = 0; i < TM; ++i) a[g][i] = lds_read_b128(stage + a_off[i] + 4 * (c ^ a_swz[i]));
+#pragma unroll
+            for (int j = 0; j < TN; ++j) b[g][j] = lds_read_b128(stage + b_off[j] + 4 * (c ^ b_swz[j]));
+        };
+        auto mfma_group = [&](int g) {
+#pragma unroll
+            for (int t = 0; t < 4; ++t)
+#pragma unroll
+                for (int i = 0; i < TM; ++i)
+#pragma unroll
+                    for (int j = 0; j < TN; ++j)
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[g][i][t], b[g][j][t], acc[i][j], 0, 0, 0);
+        };
+        read_group(0);
+        lds_wait(a[0], b[0]);
+        read_group(1);
+        pin_regs(a[0], b[0]);  // keeps group 0's MFMAs behind group 1's reads
+        mfma_group(0);
+        __builtin_amdgcn_sched_barrier(0);  // ... and group 1's wait behind group 0's MFMAs
+        lds_wait(a[1], b[1]);
+        mfma_group(1);
+    }
+
+    if (m0 + BM <= M && n0 + BN <= N) {
+        // Whole tile in range: the epilogue takes the wave's fragments at once
+        // (and can issue all of its loads before the first use).
+        ep.store_frags(z, m0 + wm * WTM, n0 + wn * WTN, row_in, khalf, acc);
+    } else {
+#pragma unroll
+        for (int j = 0; j < TN; ++j) {
+            const int n = n0 + wn * WTN + j * 32 + row_in;
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int rr = 8 * (r / 4) + 4 * khalf + (r % 4);
+#pragma unroll
+                for (int i = 0; i < TM; ++i) {
+                    const int m = m0 + wm * WTM + i * 32 + rr;
+                    if (m < M && n < N) ep.store(z, m, n, acc[i][j][r]);
+                }
+            }
+        }
+    }
+    ep.finalize(z);
+}
+
+// Launches gemm_dma_kernel; K must be a multiple of 16 and both operands
+// 16-byte aligned with row strides a multiple of 4 floats.
+template <int BM, int BN, int WAVES_M, int STAGES, class EP>
+void launch_gemm_dma(hipStream_t stream, int M, int N, int K, int batches, const KMajorRows &al, const KMajorRows &bl,
+                     const EP &ep) {
+    if (M <= 0 || N <= 0 || batches <= 0) return;
+    DMX_REQUIRE(K % 16 == 0 && K > 0, "gemm_dma: K must be a positive multiple of 16");
+    dim3 grid((unsigned)ceil_div(N, BN), (unsigned)ceil_div(M, BM), (unsigned)batches);
+    DMX_REQUIRE(grid.y <= 65535 && grid.z <= 65535, "GEMM grid too large");
+    hipLaunchKernelGGL((gemm_dma_kernel<BM, BN, WAVES_M, STAGES, EP>), grid, dim3(GEMM_THREADS), 0, stream, M, N, K,
+                       al, bl, ep);
     DMX_LAUNCH_CHECK();
 }
 

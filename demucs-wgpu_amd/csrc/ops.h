@@ -13,18 +13,32 @@ enum Act { ACT_NONE = 0, ACT_GELU = 1 };
 
 // ---------------- GEMM-based ops (conv.cu / linear.cu) ----------------
 
-// nn.Conv2d over (b, ic, h, w): weight (oc, ic, kh, kw), optional bias; act on output.
+// Convolution weights in GEMM order. A PyTorch (oc, ic, kh, kw) weight is
+// consumed in channel quads whenever conv_tap_major(ic, kh, kw): the
+// implicit-GEMM k index is (c / 4 * taps + tap) * 4 + c % 4, i.e. the weight
+// is read as (oc, ic / 4, kh * kw, 4). Four consecutive k are then four
+// channels at one tap (one bounds test per four loads), and the taps of a
+// quad follow each other, so a k-tile re-reads input rows the previous one
+// just fetched. Otherwise the PyTorch layout is used as is.
+// conv_gemm_weights() makes the GEMM-order copy (host arrays).
+inline bool conv_tap_major(int ic, int kh, int kw) { return kh * kw > 1 && ic % 4 == 0; }
+void conv_gemm_weights(const float *w, int oc, int ic, int kh, int kw, float *out);
+
+// nn.Conv2d over (b, ic, h, w): weight (oc, ic, kh, kw) in GEMM order (above),
+// optional bias; act on output.
 // `skip` (same shape as x, may be null) is added to the input while it is gathered.
 void conv2d(hipStream_t s, const float *x, const float *skip, int b, int ic, int h, int w, const float *weight,
             const float *bias, int oc, int kh, int kw, int sh, int sw, int ph, int pw, int dh, int dw, float *out,
             Act act);
 
 // nn.Conv1d over (b, ic, len) after F.pad(x, (0, len_padded - len)) (the time
-// encoder's right pad to a multiple of the stride, host.rs:633-640).
+// encoder's right pad to a multiple of the stride, host.rs:633-640); weight
+// (oc, ic, k) in GEMM order with kh = 1, kw = k.
 void conv1d_right_padded(hipStream_t s, const float *x, int b, int ic, int len, int len_padded, const float *weight,
                          const float *bias, int oc, int k, int stride, int pad, float *out, Act act);
 
-// Conv2d (any kernel, stride 1) whose 2*C output channels feed F.glu(dim=1):
+// Conv2d (any kernel, stride 1, weight in GEMM order) whose 2*C output
+// channels feed F.glu(dim=1):
 // out (b, C, oh, ow) = (y[c] + b[c]) * sigmoid(y[C+c] + b[C+c]). When `emb` is
 // given, out[b][c][f][t] += emb_scale * emb[f][c] (the frequency embedding).
 void conv2d_glu(hipStream_t s, const float *x, const float *skip, int b, int ic, int h, int w, const float *weight,
@@ -43,11 +57,13 @@ void pack_conv_transpose(const float *w, int ic, int oc, int k, int st, float *p
 // One DConv residual layer (crates/demucs-core/src/demucs/host.rs:985-1059), in
 // place on x, whose rows are (b, f) of a (B, C, F, T) tensor (F = 1 for the
 // waveform branch): conv1d k3 dilation `dil` -> GN(1) -> GELU -> 1x1 -> GN(1)
-// -> GLU -> LayerScale -> +residual. `hbuf` holds (B*F, H, T) floats, `stats`
-// 4*B*F doubles (both scratch).
-void dconv_layer(hipStream_t s, float *x, int B, int C, int F, int T, int dil, const float *w1, const float *b1,
-                 int H, const float *n1w, const float *n1b, const float *w2, const float *b2, const float *n2w,
-                 const float *n2b, const float *gamma, float *hbuf, double *stats);
+// -> GLU -> LayerScale -> +residual. `hbuf` holds dconv_hidden_floats()
+// floats, `stats` 4*B*F doubles (both scratch). w1 is the PyTorch (H, C, 3)
+// weight, w1_gemm the same in GEMM order (conv_gemm_weights with kh = 1, kw = 3).
+void dconv_layer(hipStream_t s, float *x, int B, int C, int F, int T, int dil, const float *w1,
+                 const float *w1_gemm, const float *b1, int H, const float *n1w, const float *n1b, const float *w2,
+                 const float *b2, const float *n2w, const float *n2b, const float *gamma, float *hbuf,
+                 double *stats);
 
 // The same layer with direct VALU kernels for hidden widths where MFMA tiles
 // would be mostly padding (dconv.hip); returns false when it does not apply.

@@ -136,6 +136,7 @@ struct Trace {
 struct DConvW {
     const float *w1, *b1, *n1w, *n1b, *w2, *b2, *n2w, *n2b, *gamma;
     int hidden;
+    const float *w1_gemm;  // w1 in GEMM order (conv_gemm_weights)
 };
 
 struct LayerW {
@@ -298,7 +299,8 @@ void run_dconv(dmx_runner &r, hipStream_t s, float *x, int B, int C, int F, int 
         const DConvW &D = L.dconv[d];
         DBuf h = fbuf(s, dconv_hidden_floats(rows, D.hidden, T));
         DBuf st = dbuf(s, 4 * (int64_t)rows);
-        dconv_layer(s, x, B, C, F, T, 1 << d, D.w1, D.b1, D.hidden, D.n1w, D.n1b, D.w2, D.b2, D.n2w, D.n2b, D.gamma,
+        dconv_layer(s, x, B, C, F, T, 1 << d, D.w1, D.w1_gemm, D.b1, D.hidden, D.n1w, D.n1b, D.w2, D.b2, D.n2w, D.n2b,
+                    D.gamma,
                     h.f(), st.d());
     }
     (void)r;
@@ -724,13 +726,21 @@ void load_weights(dmx_runner &r, const dmx_tensor *weights, size_t n) {
         for (size_t i = 0; i < e.size(); ++i) e[i] = t->data[i] * (float)c.emb_scale;
         r.freq_emb = upload(r, e);
     }
+    // Conv weights in GEMM order (tap-major where conv_tap_major holds).
+    auto gemm_order = [&](const std::string &name, int oc, int ic, int kh, int kw) -> const float * {
+        if (!conv_tap_major(ic, kh, kw)) return dev(r, name);
+        std::vector<float> g((size_t)oc * ic * kh * kw);
+        conv_gemm_weights(given[name]->data, oc, ic, kh, kw, g.data());
+        return upload(r, g);
+    };
     auto fill_dconv = [&](LayerW &L, const std::string &p, int ch) {
         for (int d = 0; d < 2; ++d) {
             std::string at = p + ".layers." + std::to_string(d);
+            const int hid = ch / hidden_div;
             L.dconv[d] = {dev(r, at + ".0.weight"), dev(r, at + ".0.bias"), dev(r, at + ".1.weight"),
                           dev(r, at + ".1.bias"),   dev(r, at + ".3.weight"), dev(r, at + ".3.bias"),
                           dev(r, at + ".4.weight"), dev(r, at + ".4.bias"), dev(r, at + ".6.scale"),
-                          ch / hidden_div};
+                          hid,                      gemm_order(at + ".0.weight", hid, ch, 1, 3)};
         }
     };
     chin = c.audio_channels;
@@ -740,7 +750,7 @@ void load_weights(dmx_runner &r, const dmx_tensor *weights, size_t n) {
     for (int i = 0; i < depth; ++i) {
         std::string e = "encoder." + std::to_string(i), te = "tencoder." + std::to_string(i);
         LayerW L;
-        L.conv_w = dev(r, e + ".conv.weight");
+        L.conv_w = gemm_order(e + ".conv.weight", chout_z, chin_z, 8, 1);
         L.conv_b = dev(r, e + ".conv.bias");
         L.rw = dev(r, e + ".rewrite.weight");
         L.rb = dev(r, e + ".rewrite.bias");
@@ -749,7 +759,7 @@ void load_weights(dmx_runner &r, const dmx_tensor *weights, size_t n) {
         fill_dconv(L, e + ".dconv", chout_z);
         r.enc.push_back(L);
         LayerW T;
-        T.conv_w = dev(r, te + ".conv.weight");
+        T.conv_w = gemm_order(te + ".conv.weight", chout, chin, 1, 8);
         T.conv_b = dev(r, te + ".conv.bias");
         T.rw = dev(r, te + ".rewrite.weight");
         T.rb = dev(r, te + ".rewrite.bias");
@@ -769,7 +779,7 @@ void load_weights(dmx_runner &r, const dmx_tensor *weights, size_t n) {
         L.cout = dspec[i].chout;
         L.conv_w = packed_convt(d + ".conv_tr.weight", L.cin, L.cout);
         L.conv_b = dev(r, d + ".conv_tr.bias");
-        L.rw = dev(r, d + ".rewrite.weight");
+        L.rw = gemm_order(d + ".rewrite.weight", 2 * L.cin, L.cin, 3, 3);
         L.rb = dev(r, d + ".rewrite.bias");
         fill_dconv(L, d + ".dconv", L.cin);
         r.dec.push_back(L);
@@ -778,7 +788,7 @@ void load_weights(dmx_runner &r, const dmx_tensor *weights, size_t n) {
         T.cout = tdspec[i].chout;
         T.conv_w = packed_convt(td + ".conv_tr.weight", T.cin, T.cout);
         T.conv_b = dev(r, td + ".conv_tr.bias");
-        T.rw = dev(r, td + ".rewrite.weight");
+        T.rw = gemm_order(td + ".rewrite.weight", 2 * T.cin, T.cin, 1, 3);
         T.rb = dev(r, td + ".rewrite.bias");
         fill_dconv(T, td + ".dconv", T.cin);
         r.tdec.push_back(T);
