@@ -166,6 +166,10 @@ struct dmx_runner {
     int device = 0;
     int precision = 0;
     hipStream_t stream = nullptr;
+    // The waveform branch runs on its own stream beside the spectral one
+    // (both default priority); fork/join are event waits on the GPU.
+    hipStream_t side = nullptr;
+    hipEvent_t ev_fork = nullptr, ev_join = nullptr;
     std::string tag;
     int64_t training_length = 0;
     int hop = 0, pre_channels = 0, tch = 0, hidden = 0, freq_emb_rows = 0;
@@ -215,6 +219,31 @@ void record(dmx_runner &r, const std::string &name, const float *d, std::initial
     DMX_HIP(hipMemcpy(host.data(), d, (size_t)n * sizeof(float), hipMemcpyDeviceToHost));
     r.trace.record(name.c_str(), s.data(), (int32_t)s.size(), host.data(), r.trace.user);
 }
+
+// The two branches of the forward (spectral on `s`, waveform on `t`). They
+// only meet at the transformer's cross layers and at the final sum, so the
+// waveform work runs on the runner's side stream between fork() (t waits for
+// everything enqueued on s so far) and join() (s waits for everything on t).
+// Buffer rule: a buffer that work on both streams touches comes from s's
+// pool, is taken before the fork and released after the join; a buffer only
+// t's work touches comes from t's pool. With a trace sink the whole forward
+// stays on s (record() reads activations in stream order).
+struct Branches {
+    dmx_runner &r;
+    hipStream_t s, t;
+    Branches(dmx_runner &runner, hipStream_t main)
+        : r(runner), s(main), t(runner.trace.record || !runner.side ? main : runner.side) {}
+    void fork() {
+        if (t == s) return;
+        DMX_HIP(hipEventRecord(r.ev_fork, s));
+        DMX_HIP(hipStreamWaitEvent(t, r.ev_fork, 0));
+    }
+    void join() {
+        if (t == s) return;
+        DMX_HIP(hipEventRecord(r.ev_join, t));
+        DMX_HIP(hipStreamWaitEvent(s, r.ev_join, 0));
+    }
+};
 
 // `HtdemucsConfig::validate` (crates/demucs-core/src/demucs/config.rs:239-273).
 void validate(const dmx_config &c) {
@@ -307,9 +336,10 @@ void run_dconv(dmx_runner &r, hipStream_t s, float *x, int B, int C, int F, int 
 }
 
 // One `classic_layer_forward` / `cross_layer_forward` (host.rs:1315-1429) on
-// token planes; returns the new plane (GroupNorm applied).
-DBuf transformer_layer(dmx_runner &r, hipStream_t s, const TLayerW &L, const float *xq, int64_t Lq, const float *xkv,
-                       int64_t Lk, int B, const std::string &name) {
+// token planes, on stream s; writes the new plane (GroupNorm applied) to out
+// (B, Lq, D). Its temporaries come from s's pool.
+void transformer_layer(dmx_runner &r, hipStream_t s, const TLayerW &L, const float *xq, int64_t Lq, const float *xkv,
+                       int64_t Lk, int B, const std::string &name, float *out) {
     const int D = r.tch, H = r.hidden, heads = r.cfg.t_heads;
     const float scale = 1.0f / std::sqrt((float)(D / heads));
     DBuf nq = fbuf(s, B * Lq * D);
@@ -343,14 +373,34 @@ DBuf transformer_layer(dmx_runner &r, hipStream_t s, const TLayerW &L, const flo
     DBuf hid = fbuf(s, B * Lq * H);
     linear(s, n2.f(), D, Lq * D, L.w1, L.b1, B, (int)Lq, D, H, hid.f(), H, Lq * H, TAIL_BIAS_GELU, nullptr, nullptr,
            nullptr);
-    DBuf out = fbuf(s, B * Lq * D);
     DBuf stats = dbuf(s, 2 * B);
     zero_doubles(s, stats.d(), 2 * B);
-    linear(s, hid.f(), H, Lq * H, L.w2, L.b2, B, (int)Lq, H, D, out.f(), D, Lq * D, TAIL_RESIDUAL_SCALE, x1.f(), L.g2,
+    linear(s, hid.f(), H, Lq * H, L.w2, L.b2, B, (int)Lq, H, D, out, D, Lq * D, TAIL_RESIDUAL_SCALE, x1.f(), L.g2,
            stats.d());
-    group_norm_tokens_apply(s, out.f(), B, (int)Lq, D, stats.d(), L.now_, L.nob);
-    record(r, name, out.f(), {B, Lq, D});
-    return out;
+    group_norm_tokens_apply(s, out, B, (int)Lq, D, stats.d(), L.now_, L.nob);
+    record(r, name, out, {B, Lq, D});
+}
+
+// The layers of the cross-transformer (host.rs:895-941) on the token planes
+// spec (B, Lf, D) and time (B, Lt, D), which are replaced by the outputs.
+// Layer i of the two branches runs concurrently: the waveform layer on the
+// side stream, reading the spectral plane of layer i - 1 (cross layers).
+void transformer_layers(dmx_runner &r, hipStream_t s, DBuf &spec, int64_t Lf, DBuf &time, int64_t Lt, int B) {
+    const int D = r.tch;
+    for (int i = 0; i < r.cfg.t_layers; ++i) {
+        std::string n = "crosstransformer.layers." + std::to_string(i);
+        std::string nt = "crosstransformer.layers_t." + std::to_string(i);
+        const bool cross = r.layers[i].cross;
+        DBuf ns = fbuf(s, B * Lf * D), nt_ = fbuf(s, (int64_t)B * Lt * D);
+        Branches br(r, s);
+        br.fork();
+        transformer_layer(r, br.t, r.layers_t[i], time.f(), Lt, cross ? spec.f() : nullptr, cross ? Lf : 0, B, nt,
+                          nt_.f());
+        transformer_layer(r, s, r.layers[i], spec.f(), Lf, cross ? time.f() : nullptr, cross ? Lt : 0, B, n, ns.f());
+        br.join();
+        spec = std::move(ns);
+        time = std::move(nt_);
+    }
 }
 
 // `transformer_forward` (host.rs:830-946): x (B, D, F, T), xt (B, D, Lt) channel-major.
@@ -366,19 +416,7 @@ void transformer(dmx_runner &r, hipStream_t s, const float *x, const float *xt, 
                           dev(r, "crosstransformer.norm_in_t.bias"), pos1d_for(r, Lt), wpe, time.f());
     record(r, "crosstransformer.in#0", spec.f(), {B, Lf, D});
     record(r, "crosstransformer.in#1", time.f(), {B, Lt, D});
-    for (int i = 0; i < r.cfg.t_layers; ++i) {
-        std::string n = "crosstransformer.layers." + std::to_string(i);
-        std::string nt = "crosstransformer.layers_t." + std::to_string(i);
-        if (r.layers[i].cross) {
-            DBuf ns = transformer_layer(r, s, r.layers[i], spec.f(), Lf, time.f(), Lt, B, n);
-            DBuf nt_ = transformer_layer(r, s, r.layers_t[i], time.f(), Lt, spec.f(), Lf, B, nt);
-            spec = std::move(ns);
-            time = std::move(nt_);
-        } else {
-            spec = transformer_layer(r, s, r.layers[i], spec.f(), Lf, nullptr, 0, B, n);
-            time = transformer_layer(r, s, r.layers_t[i], time.f(), Lt, nullptr, 0, B, nt);
-        }
-    }
+    transformer_layers(r, s, spec, Lf, time, Lt, B);
     // The channel downsamplers read the token planes directly.
     tokens_to_channels(s, spec.f(), B, F, T, D, dev(r, "channel_downsampler.weight"), dev(r, "channel_downsampler.bias"),
                        r.pre_channels, x_out);
@@ -404,19 +442,7 @@ void transformer_only(dmx_runner &r, hipStream_t s, const float *x, const float 
                           dev(r, "crosstransformer.norm_in.bias"), pos2d_for(r, F, T), wpe, spec.f());
     channels_to_tokens_ln(s, xt, B, D, 1, Lt, dev(r, "crosstransformer.norm_in_t.weight"),
                           dev(r, "crosstransformer.norm_in_t.bias"), pos1d_for(r, Lt), wpe, time.f());
-    for (int i = 0; i < r.cfg.t_layers; ++i) {
-        std::string n = "crosstransformer.layers." + std::to_string(i);
-        std::string nt = "crosstransformer.layers_t." + std::to_string(i);
-        if (r.layers[i].cross) {
-            DBuf ns = transformer_layer(r, s, r.layers[i], spec.f(), Lf, time.f(), Lt, B, n);
-            DBuf nt_ = transformer_layer(r, s, r.layers_t[i], time.f(), Lt, spec.f(), Lf, B, nt);
-            spec = std::move(ns);
-            time = std::move(nt_);
-        } else {
-            spec = transformer_layer(r, s, r.layers[i], spec.f(), Lf, nullptr, 0, B, n);
-            time = transformer_layer(r, s, r.layers_t[i], time.f(), Lt, nullptr, 0, B, nt);
-        }
-    }
+    transformer_layers(r, s, spec, Lf, time, Lt, B);
     // The rearrange back to (B, D, F, T) reuses the token-gather GEMM with an
     // identity matrix (exact: every output is one product by 1.0 plus zeros).
     if (!r.eye) {
@@ -445,27 +471,44 @@ void forward_full(dmx_runner &r, hipStream_t s, const float *mix, int B, float *
 
     const int depth = c.depth;
     std::vector<DBuf> saved, saved_t;
-    std::vector<int> lengths_t, fdims;
-    // Each encoder layer reads the previous layer's output, which is also the
-    // skip connection kept in saved / saved_t.
-    const float *x_in = xspec.f(), *xt_in = xwave.f();
-    int cin = 4, F = bins, tcin = 2, tlen = L;
+    std::vector<int> lengths_t;
+    // The waveform encoder's outputs are also the waveform decoder's skips:
+    // s's pool, taken before the fork, released after the decoder's join.
+    int tlen = L;
     for (int i = 0; i < depth; ++i) {
-        // Waveform encoder (host.rs:625-678).
-        const LayerW &TL = r.tenc[i];
         lengths_t.push_back(tlen);
-        int padded = tlen % 4 ? tlen + (4 - tlen % 4) : tlen;
-        int tout = (padded + 4 - 8) / 4 + 1;
-        DBuf y = fbuf(s, (int64_t)B * TL.cout * tout);
-        conv1d_right_padded(s, xt_in, B, tcin, tlen, padded, TL.conv_w, TL.conv_b, TL.cout, 8, 4, 2, y.f(), ACT_GELU);
-        run_dconv(r, s, y.f(), B, TL.cout, 1, tout, TL);
-        DBuf xt_next = fbuf(s, (int64_t)B * TL.cout * tout);
-        conv2d_glu(s, y.f(), nullptr, B, TL.cout, 1, tout, TL.rw, TL.rb, TL.cout, 1, 1, 0, 0, xt_next.f(), nullptr, 0.f);
-        tcin = TL.cout;
-        tlen = tout;
-        record(r, "tencoder." + std::to_string(i), xt_next.f(), {B, tcin, tlen});
-        xt_in = xt_next.f();
-        saved_t.push_back(std::move(xt_next));
+        const int padded = tlen % 4 ? tlen + (4 - tlen % 4) : tlen;
+        tlen = (padded + 4 - 8) / 4 + 1;
+        saved_t.push_back(fbuf(s, (int64_t)B * r.tenc[i].cout * tlen));
+    }
+    Branches enc(r, s);
+    enc.fork();
+    {
+        // Waveform encoder (host.rs:625-678) on the side stream.
+        const hipStream_t t = enc.t;
+        const float *xt_in = xwave.f();
+        int tcin = 2;
+        for (int i = 0; i < depth; ++i) {
+            const LayerW &TL = r.tenc[i];
+            const int len = lengths_t[i];
+            const int padded = len % 4 ? len + (4 - len % 4) : len;
+            const int tout = (padded + 4 - 8) / 4 + 1;
+            DBuf y = fbuf(t, (int64_t)B * TL.cout * tout);
+            conv1d_right_padded(t, xt_in, B, tcin, len, padded, TL.conv_w, TL.conv_b, TL.cout, 8, 4, 2, y.f(),
+                                ACT_GELU);
+            run_dconv(r, t, y.f(), B, TL.cout, 1, tout, TL);
+            conv2d_glu(t, y.f(), nullptr, B, TL.cout, 1, tout, TL.rw, TL.rb, TL.cout, 1, 1, 0, 0, saved_t[i].f(),
+                       nullptr, 0.f);
+            tcin = TL.cout;
+            record(r, "tencoder." + std::to_string(i), saved_t[i].f(), {B, tcin, tout});
+            xt_in = saved_t[i].f();
+        }
+    }
+    // Each encoder layer reads the previous layer's output, which is also the
+    // skip connection kept in saved.
+    const float *x_in = xspec.f();
+    int cin = 4, F = bins;
+    for (int i = 0; i < depth; ++i) {
         // Frequency encoder (host.rs:577-622).
         const LayerW &FL = r.enc[i];
         int fout = (F + 4 - 8) / 4 + 1;
@@ -485,6 +528,7 @@ void forward_full(dmx_runner &r, hipStream_t s, const float *mix, int B, float *
         x_in = x_next.f();
         saved.push_back(std::move(x_next));
     }
+    enc.join();
     xspec.release();
     xwave.release();
     const float *xin = saved.back().f();
@@ -505,9 +549,40 @@ void forward_full(dmx_runner &r, hipStream_t s, const float *mix, int B, float *
     record(r, "channel_downsampler", xd.f(), {B, P, (int64_t)F * le});
     record(r, "channel_downsampler_t", xtd.f(), {B, P, tlen});
 
-    DBuf x = std::move(xd), xt = std::move(xtd);
+    // Decoders: the waveform branch on the side stream again. Its last
+    // output feeds the final sum on s, so it comes from s's pool.
+    DBuf xt_out = fbuf(s, (int64_t)B * c.sources * 2 * L);
+    Branches dec(r, s);
+    dec.fork();
+    {
+        // Waveform decoder (host.rs:763-827).
+        const hipStream_t t = dec.t;
+        const float *xt_in = xtd.f();
+        DBuf cur;  // the previous layer's output (side-stream pool)
+        int tcin = P;
+        for (int i = 0; i < depth; ++i) {
+            const bool last = i == depth - 1;
+            const LayerW &TL = r.tdec[i];
+            const float *skip_t = saved_t[depth - 1 - i].f();
+            const int length_t = lengths_t[depth - 1 - i];
+            DBuf gt = fbuf(t, (int64_t)B * tcin * tlen);
+            conv2d_glu(t, xt_in, skip_t, B, tcin, 1, tlen, TL.rw, TL.rb, tcin, 1, 3, 0, 1, gt.f(), nullptr, 0.f);
+            run_dconv(r, t, gt.f(), B, tcin, 1, tlen, TL);
+            record(r, "tdecoder." + std::to_string(i) + "#1", gt.f(), {B, tcin, tlen});
+            DBuf zt = last ? DBuf() : fbuf(t, (int64_t)B * TL.cout * length_t);
+            float *zt_p = last ? xt_out.f() : zt.f();
+            conv_transpose_axis(t, gt.f(), B, tcin, tlen, 1, TL.conv_w, TL.conv_b, TL.cout, 8, 4, 2, length_t, zt_p,
+                                last ? ACT_NONE : ACT_GELU);
+            record(r, "tdecoder." + std::to_string(i) + "#0", zt_p, {B, TL.cout, length_t});
+            cur = std::move(zt);
+            xt_in = zt_p;
+            tcin = TL.cout;
+            tlen = length_t;
+        }
+        DMX_REQUIRE(tcin == c.sources * 2 && tlen == L, "waveform decoder output shape is wrong");
+    }
+    DBuf x = std::move(xd);
     cin = P;
-    tcin = P;
     for (int i = 0; i < depth; ++i) {
         const bool last = i == depth - 1;
         // Frequency decoder (host.rs:682-759).
@@ -527,26 +602,12 @@ void forward_full(dmx_runner &r, hipStream_t s, const float *mix, int B, float *
         x = std::move(z);
         cin = FL.cout;
         F = fout;
-        // Waveform decoder (host.rs:763-827).
-        const LayerW &TL = r.tdec[i];
-        DBuf skip_t = std::move(saved_t.back());
-        saved_t.pop_back();
-        int length_t = lengths_t.back();
-        lengths_t.pop_back();
-        DBuf gt = fbuf(s, (int64_t)B * tcin * tlen);
-        conv2d_glu(s, xt.f(), skip_t.f(), B, tcin, 1, tlen, TL.rw, TL.rb, tcin, 1, 3, 0, 1, gt.f(), nullptr, 0.f);
-        skip_t.release();
-        run_dconv(r, s, gt.f(), B, tcin, 1, tlen, TL);
-        record(r, "tdecoder." + std::to_string(i) + "#1", gt.f(), {B, tcin, tlen});
-        DBuf zt = fbuf(s, (int64_t)B * TL.cout * length_t);
-        conv_transpose_axis(s, gt.f(), B, tcin, tlen, 1, TL.conv_w, TL.conv_b, TL.cout, 8, 4, 2, length_t, zt.f(),
-                            last ? ACT_NONE : ACT_GELU);
-        record(r, "tdecoder." + std::to_string(i) + "#0", zt.f(), {B, TL.cout, length_t});
-        xt = std::move(zt);
-        tcin = TL.cout;
-        tlen = length_t;
     }
-    DMX_REQUIRE(cin == c.sources * 4 && tcin == c.sources * 2 && tlen == L, "decoder output shapes are wrong");
+    dec.join();
+    saved_t.clear();
+    xtd.release();
+    DMX_REQUIRE(cin == c.sources * 4, "decoder output shapes are wrong");
+    const DBuf &xt = xt_out;
     const int S = c.sources, rows = B * S * 2;
     DBuf scratch = fbuf(s, (int64_t)rows * le * nfft + (int64_t)rows * le * bins * 2);
     ispec_and_sum(s, x.f(), xt.f(), B, S, L, nfft, le, norms.f(), scratch.f(), stems, r.twiddles);
@@ -1058,9 +1119,15 @@ int dmx_runner_create(const dmx_tensor *weights, size_t n_weights, const dmx_con
         DMX_HIP(hipGetDeviceProperties(&prop, device_ordinal));
         r->tag = std::string("hip:") + prop.name + ":" + prop.gcnArchName;
         DMX_HIP(hipStreamCreateWithFlags(&r->stream, hipStreamNonBlocking));
+        DMX_HIP(hipStreamCreateWithFlags(&r->side, hipStreamNonBlocking));
+        DMX_HIP(hipEventCreateWithFlags(&r->ev_fork, hipEventDisableTiming));
+        DMX_HIP(hipEventCreateWithFlags(&r->ev_join, hipEventDisableTiming));
         load_weights(*r, weights, n_weights);
     });
     if (rc != DMX_OK) {
+        if (r->ev_fork) (void)hipEventDestroy(r->ev_fork);
+        if (r->ev_join) (void)hipEventDestroy(r->ev_join);
+        if (r->side) (void)hipStreamDestroy(r->side);
         if (r->stream) (void)hipStreamDestroy(r->stream);
         if (r->weight_mem) (void)hipFree(r->weight_mem);
         for (void *p : r->owned) (void)hipFree(p);
@@ -1073,12 +1140,16 @@ int dmx_runner_create(const dmx_tensor *weights, size_t n_weights, const dmx_con
 void dmx_runner_destroy(dmx_runner *r) {
     if (!r) return;
     (void)hipSetDevice(r->device);
-    if (r->stream) {
-        (void)hipStreamSynchronize(r->stream);
-        StreamPool::instance().trim(r->stream);
-    }
+    for (hipStream_t st : {r->stream, r->side})
+        if (st) {
+            (void)hipStreamSynchronize(st);
+            StreamPool::instance().trim(st);
+        }
     if (r->weight_mem) (void)hipFree(r->weight_mem);
     for (void *p : r->owned) (void)hipFree(p);
+    if (r->ev_fork) (void)hipEventDestroy(r->ev_fork);
+    if (r->ev_join) (void)hipEventDestroy(r->ev_join);
+    if (r->side) (void)hipStreamDestroy(r->side);
     if (r->stream) (void)hipStreamDestroy(r->stream);
     delete r;
 }
