@@ -483,12 +483,19 @@ void forward_full(dmx_runner &r, hipStream_t s, const float *mix, int B, float *
     }
     Branches enc(r, s);
     enc.fork();
-    {
-        // Waveform encoder (host.rs:625-678) on the side stream.
-        const hipStream_t t = enc.t;
-        const float *xt_in = xwave.f();
-        int tcin = 2;
-        for (int i = 0; i < depth; ++i) {
+    // Layer i of both encoders is enqueued together (the waveform layer on
+    // the side stream), so neither stream waits for the host to enqueue the
+    // other branch's whole encoder.
+    const float *xt_in = xwave.f();
+    int tcin = 2;
+    // Each encoder layer reads the previous layer's output, which is also the
+    // skip connection kept in saved.
+    const float *x_in = xspec.f();
+    int cin = 4, F = bins;
+    for (int i = 0; i < depth; ++i) {
+        {
+            // Waveform encoder (host.rs:625-678).
+            const hipStream_t t = enc.t;
             const LayerW &TL = r.tenc[i];
             const int len = lengths_t[i];
             const int padded = len % 4 ? len + (4 - len % 4) : len;
@@ -503,12 +510,6 @@ void forward_full(dmx_runner &r, hipStream_t s, const float *mix, int B, float *
             record(r, "tencoder." + std::to_string(i), saved_t[i].f(), {B, tcin, tout});
             xt_in = saved_t[i].f();
         }
-    }
-    // Each encoder layer reads the previous layer's output, which is also the
-    // skip connection kept in saved.
-    const float *x_in = xspec.f();
-    int cin = 4, F = bins;
-    for (int i = 0; i < depth; ++i) {
         // Frequency encoder (host.rs:577-622).
         const LayerW &FL = r.enc[i];
         int fout = (F + 4 - 8) / 4 + 1;
@@ -554,37 +555,35 @@ void forward_full(dmx_runner &r, hipStream_t s, const float *mix, int B, float *
     DBuf xt_out = fbuf(s, (int64_t)B * c.sources * 2 * L);
     Branches dec(r, s);
     dec.fork();
-    {
-        // Waveform decoder (host.rs:763-827).
-        const hipStream_t t = dec.t;
-        const float *xt_in = xtd.f();
-        DBuf cur;  // the previous layer's output (side-stream pool)
-        int tcin = P;
-        for (int i = 0; i < depth; ++i) {
-            const bool last = i == depth - 1;
-            const LayerW &TL = r.tdec[i];
-            const float *skip_t = saved_t[depth - 1 - i].f();
-            const int length_t = lengths_t[depth - 1 - i];
-            DBuf gt = fbuf(t, (int64_t)B * tcin * tlen);
-            conv2d_glu(t, xt_in, skip_t, B, tcin, 1, tlen, TL.rw, TL.rb, tcin, 1, 3, 0, 1, gt.f(), nullptr, 0.f);
-            run_dconv(r, t, gt.f(), B, tcin, 1, tlen, TL);
-            record(r, "tdecoder." + std::to_string(i) + "#1", gt.f(), {B, tcin, tlen});
-            DBuf zt = last ? DBuf() : fbuf(t, (int64_t)B * TL.cout * length_t);
-            float *zt_p = last ? xt_out.f() : zt.f();
-            conv_transpose_axis(t, gt.f(), B, tcin, tlen, 1, TL.conv_w, TL.conv_b, TL.cout, 8, 4, 2, length_t, zt_p,
-                                last ? ACT_NONE : ACT_GELU);
-            record(r, "tdecoder." + std::to_string(i) + "#0", zt_p, {B, TL.cout, length_t});
-            cur = std::move(zt);
-            xt_in = zt_p;
-            tcin = TL.cout;
-            tlen = length_t;
-        }
-        DMX_REQUIRE(tcin == c.sources * 2 && tlen == L, "waveform decoder output shape is wrong");
-    }
+    // Layer i of both decoders is enqueued together, the waveform layer on
+    // the side stream.
+    const float *xt_in2 = xtd.f();
+    DBuf cur;  // the waveform decoder's previous output (side-stream pool)
+    int tc = P;
     DBuf x = std::move(xd);
     cin = P;
     for (int i = 0; i < depth; ++i) {
         const bool last = i == depth - 1;
+        {
+            // Waveform decoder (host.rs:763-827).
+            const hipStream_t t = dec.t;
+            const LayerW &TL = r.tdec[i];
+            const float *skip_t = saved_t[depth - 1 - i].f();
+            const int length_t = lengths_t[depth - 1 - i];
+            DBuf gt = fbuf(t, (int64_t)B * tc * tlen);
+            conv2d_glu(t, xt_in2, skip_t, B, tc, 1, tlen, TL.rw, TL.rb, tc, 1, 3, 0, 1, gt.f(), nullptr, 0.f);
+            run_dconv(r, t, gt.f(), B, tc, 1, tlen, TL);
+            record(r, "tdecoder." + std::to_string(i) + "#1", gt.f(), {B, tc, tlen});
+            DBuf zt = last ? DBuf() : fbuf(t, (int64_t)B * TL.cout * length_t);
+            float *zt_p = last ? xt_out.f() : zt.f();
+            conv_transpose_axis(t, gt.f(), B, tc, tlen, 1, TL.conv_w, TL.conv_b, TL.cout, 8, 4, 2, length_t, zt_p,
+                                last ? ACT_NONE : ACT_GELU);
+            record(r, "tdecoder." + std::to_string(i) + "#0", zt_p, {B, TL.cout, length_t});
+            cur = std::move(zt);
+            xt_in2 = zt_p;
+            tc = TL.cout;
+            tlen = length_t;
+        }
         // Frequency decoder (host.rs:682-759).
         const LayerW &FL = r.dec[i];
         DBuf skip = std::move(saved.back());
@@ -603,6 +602,7 @@ void forward_full(dmx_runner &r, hipStream_t s, const float *mix, int B, float *
         cin = FL.cout;
         F = fout;
     }
+    DMX_REQUIRE(tc == c.sources * 2 && tlen == L, "waveform decoder output shape is wrong");
     dec.join();
     saved_t.clear();
     xtd.release();

@@ -12,6 +12,8 @@
 // Only the le kept frames are ever transformed: every sample they read lies
 // inside the reflect-padded signal, so the centre padding is never touched,
 // and the four zero frames of the inverse only add window energy.
+#include <algorithm>
+
 #include "common.h"
 #include "ops.h"
 
@@ -79,17 +81,43 @@ __global__ __launch_bounds__(FFT_THREADS) void stft_kernel(const float *__restri
     }
 }
 
-// f64 (sum, sum of squares) per batch over `len` floats.
+// f64 (sum, sum of squares) over `len` floats per batch row blockIdx.y,
+// added into stats[stats_stride * row]. VEC: len a multiple of 4 and rows
+// 16-byte aligned, read as float4.
+template <bool VEC>
 __global__ __launch_bounds__(256) void batch_moments_kernel(const float *__restrict__ x, int64_t len,
-                                                            double *__restrict__ stats) {
-    const float *p = x + (int64_t)blockIdx.y * len;
+                                                            double *__restrict__ stats, int stats_stride) {
+    const float *row = x + (int64_t)blockIdx.y * len;
     double s = 0.0, q = 0.0;
-    for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < len; i += (int64_t)gridDim.x * 256) {
-        double v = p[i];
-        s += v;
-        q += v * v;
+    if constexpr (VEC) {
+        const float4 *p = reinterpret_cast<const float4 *>(row);
+        for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < len / 4; i += (int64_t)gridDim.x * 256) {
+            const float4 v = p[i];
+            const double a = v.x, b = v.y, c = v.z, d = v.w;
+            s += (a + b) + (c + d);
+            q += (a * a + b * b) + (c * c + d * d);
+        }
+    } else {
+        for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < len; i += (int64_t)gridDim.x * 256) {
+            const double v = row[i];
+            s += v;
+            q += v * v;
+        }
     }
-    block_moments_atomic(s, q, stats + 2 * blockIdx.y);
+    block_moments_atomic(s, q, stats + (int64_t)stats_stride * blockIdx.y);
+}
+
+// Moments of b rows of len floats in one launch (grid.y = row).
+void batch_moments(hipStream_t s, const float *x, int b, int64_t len, double *stats, int stats_stride) {
+    const unsigned per_row = (unsigned)std::max<int64_t>(1, std::min<int64_t>(2048 / std::max(b, 1), 256));
+    const bool vec = len % 4 == 0 && (reinterpret_cast<uintptr_t>(x) & 15) == 0;
+    if (vec)
+        hipLaunchKernelGGL(batch_moments_kernel<true>, dim3(per_row, (unsigned)b), dim3(256), 0, s, x, len, stats,
+                           stats_stride);
+    else
+        hipLaunchKernelGGL(batch_moments_kernel<false>, dim3(per_row, (unsigned)b), dim3(256), 0, s, x, len, stats,
+                           stats_stride);
+    DMX_LAUNCH_CHECK();
 }
 
 // mean and unbiased std per batch (`mean` / `std_unbiased`, demucs/ops.rs:1494-1509, 1585-1590).
@@ -269,15 +297,10 @@ void spec_and_normalise(hipStream_t s, const float *mix, int b, int L, int nfft,
     // stats layout per batch: (sum, sumsq) spectrum, then (sum, sumsq) wave.
     zero_doubles(s, stats, 4 * (int64_t)b);
     const int64_t spec_len = (int64_t)2 * le * bins * 2;  // 2 channels x le x bins x (re, im)
-    for (int bi = 0; bi < b; ++bi) {
-        hipLaunchKernelGGL(batch_moments_kernel, dim3(grid_cap(spec_len, 1024), 1), dim3(256), 0, s,
-                           frames + bi * spec_len, spec_len, stats + 4 * bi);
-        DMX_LAUNCH_CHECK();
-        hipLaunchKernelGGL(batch_moments_kernel, dim3(grid_cap(2 * (int64_t)L, 1024), 1), dim3(256), 0, s,
-                           mix + (int64_t)bi * 2 * L, 2 * (int64_t)L, stats + 4 * bi + 2);
-        DMX_LAUNCH_CHECK();
-    }
     DMX_REQUIRE(b <= 1024, "spec_and_normalise: batch too large");
+    // One launch per tensor for all batch rows.
+    batch_moments(s, frames, b, spec_len, stats, 4);
+    batch_moments(s, mix, b, 2 * (int64_t)L, stats + 2, 4);
     hipLaunchKernelGGL(finish_norms_kernel, dim3(1), dim3(1024), 0, s, stats, b, (double)spec_len, 2.0 * L, norms);
     DMX_LAUNCH_CHECK();
     hipLaunchKernelGGL(spec_normalise_kernel, dim3((unsigned)ceil_div(le, 32), (unsigned)(bins / 32), (unsigned)(b * 2)),
