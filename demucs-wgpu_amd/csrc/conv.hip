@@ -157,34 +157,41 @@ struct NormGeluQuads {
     }
 };
 
-// Transposed convolution along one axis, one output phase per problem:
-// z = b * st + p; output positions a' = st*q + p - crop with q = qmin(p) + n / P.
-// Tap j of input row q - j meets kernel index p + st*j.
-template <int TAPS>
+// Transposed convolution (kernel = 2 * stride) along one axis, every output
+// phase in one GEMM: B[k][n] with k = 2 c + j (input channel c, tap j) and
+// column n = qi * P + t is x[b][c][q - j][t] with q = q0 + qi, zero outside
+// [0, A). Each input value then feeds 2 k-rows (its two taps) instead of one
+// per (phase, tap) pair. A quad of k is two channels x two taps.
 struct ConvTGather {
     static constexpr bool kmajor = false;
     __device__ bool fast() const { return true; }
     const float *x;
-    int ic, A, P, st, crop;
+    int ic, A, P, q0;
     struct State {
         const float *base;
         int q;
     };
     __device__ State setup(int z, int n) const {
-        int b = z / st, p = z - b * st;
-        int qmin = crop > p ? (crop - p + st - 1) / st : 0;
-        int qi = n / P, t = n - qi * P;
-        return {x + (int64_t)b * ic * A * P + t, qmin + qi};
+        const int qi = n / P, t = n - qi * P;
+        return {x + (int64_t)z * ic * A * P + t, q0 + qi};
     }
-    __device__ float load(const State &s, int k) const {
-        int c = k / TAPS, j = k - c * TAPS;
-        int a = s.q - j;
-        if (a < 0 || a >= A) return 0.0f;
-        return s.base[((int64_t)c * A + a) * P];
+    __device__ float4 load_quad(const State &s, int k) const {
+        const int c = k >> 1;
+        const bool in0 = s.q >= 0 && s.q < A, in1 = s.q >= 1 && s.q - 1 < A;
+        const float *p0 = s.base + ((int64_t)c * A + s.q) * P;  // channel c, row q
+        const int64_t cstride = (int64_t)A * P;
+        float4 v;
+        v.x = in0 ? p0[0] : 0.f;
+        v.y = in1 ? p0[-P] : 0.f;
+        v.z = in0 ? p0[cstride] : 0.f;
+        v.w = in1 ? p0[cstride - P] : 0.f;
+        return v;
     }
 };
 
-// Phase-packed transposed-conv weights: (st, oc, ic*taps), k-major rows.
+// Phase-packed transposed-conv weights (st, oc, ic*taps), read as the rows
+// m = o * st + p (output channel o, phase p) of one (oc * st, ic * taps)
+// matrix; k-major rows.
 struct PhaseWeights {
     static constexpr bool kmajor = true;
     const float *w;
@@ -193,7 +200,10 @@ struct PhaseWeights {
     struct State {
         const float *row;
     };
-    __device__ State setup(int z, int m) const { return {w + ((int64_t)(z % st) * oc + m) * K}; }
+    __device__ State setup(int, int m) const {
+        const int o = m / st, p = m - o * st;
+        return {w + ((int64_t)p * oc + o) * K};
+    }
     __device__ bool fast() const { return vec; }
     __device__ float4 load4_full(const State &s, int k) const { return *reinterpret_cast<const float4 *>(s.row + k); }
     __device__ float4 load4(const State &s, int k, int Kt) const {
@@ -267,18 +277,19 @@ struct EpGlu : EpBase {
     }
 };
 
-// Transposed-conv output: scatter phase rows back into the cropped axis.
+// Transposed-conv output: row m = o * st + p, column n = qi * P + t is
+// output position a = st * (q0 + qi) + p - crop of channel o (dropped
+// outside the crop [0, a_out)).
 struct EpConvT : EpBase {
     float *out;
     const float *bias;
-    int oc, st, crop, a_out, P, act;
+    int oc, st, crop, a_out, P, q0, act;
     __device__ void store(int z, int m, int n, float v) {
-        int b = z / st, p = z - b * st;
-        int qmin = crop > p ? (crop - p + st - 1) / st : 0;
-        int qi = n / P, t = n - qi * P;
-        int a = st * (qmin + qi) + p - crop;
-        if (a >= a_out) return;
-        out[(((int64_t)b * oc + m) * a_out + a) * P + t] = act_apply(act, v + bias[m]);
+        const int o = m / st, p = m - o * st;
+        const int qi = n / P, t = n - qi * P;
+        const int a = st * (q0 + qi) + p - crop;
+        if (a < 0 || a >= a_out) return;
+        out[(((int64_t)z * oc + o) * a_out + a) * P + t] = act_apply(act, v + bias[o]);
     }
 };
 
@@ -663,16 +674,14 @@ void conv_transpose_axis(hipStream_t s, const float *x, int b, int ic, int A, in
                          const float *bias, int oc, int k, int st, int crop, int a_out, float *out, Act act) {
     require_ptrs({x, weight_packed, bias, out}, "conv_transpose_axis");
     int taps = conv_transpose_taps(k, st);
-    DMX_REQUIRE(taps == 2, "conv_transpose_axis: only kernel = 2 * stride is supported");
-    DMX_REQUIRE(crop + a_out <= (A - 1) * st + k, "conv_transpose_axis: crop past the produced length");
-    int max_count = 0;
-    for (int p = 0; p < st; ++p) {
-        int qmin = crop > p ? (crop - p + st - 1) / st : 0;
-        int qend = (a_out + crop - p + st - 1) / st;
-        max_count = std::max(max_count, qend - qmin);
-    }
-    int K = ic * taps, N = max_count * P;
-    ConvTGather<2> g{x, ic, A, P, st, crop};
+    DMX_REQUIRE(taps == 2 && k == 2 * st, "conv_transpose_axis: only kernel = 2 * stride is supported");
+    DMX_REQUIRE(crop >= 0 && crop + a_out <= (A - 1) * st + k, "conv_transpose_axis: crop past the produced length");
+    DMX_REQUIRE(ic % 2 == 0, "conv_transpose_axis: the input channel count must be even (k quads are 2 channels)");
+    // Input rows q cover every kept output a = st * q + p - crop, p < st.
+    const int q0 = crop >= st - 1 ? (crop - (st - 1) + st - 1) / st : 0;
+    const int q_end = (a_out + crop + st - 1) / st;
+    const int K = ic * taps, N = (q_end - q0) * P, M = oc * st;
+    ConvTGather g{x, ic, A, P, q0};
     PhaseWeights pw{weight_packed, st, oc, K, aligned16(weight_packed) && K % 4 == 0};
     EpConvT ep;
     ep.out = out;
@@ -682,8 +691,9 @@ void conv_transpose_axis(hipStream_t s, const float *x, int b, int ic, int A, in
     ep.crop = crop;
     ep.a_out = a_out;
     ep.P = P;
+    ep.q0 = q0;
     ep.act = act;
-    gemm_auto<false>(s, oc, N, K, b * st, pw, g, ep);
+    gemm_auto<false>(s, M, N, K, b, pw, g, ep);
 }
 
 void dconv_layer(hipStream_t s, float *x, int B, int C, int F, int T, int dil, const float *w1,

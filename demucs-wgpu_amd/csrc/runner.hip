@@ -12,6 +12,7 @@
 
 #include <algorithm>
 #include <cmath>
+#include <cstdlib>
 #include <cstring>
 #include <map>
 #include <memory>
@@ -227,12 +228,22 @@ void record(dmx_runner &r, const std::string &name, const float *d, std::initial
 // Buffer rule: a buffer that work on both streams touches comes from s's
 // pool, is taken before the fork and released after the join; a buffer only
 // t's work touches comes from t's pool. With a trace sink the whole forward
-// stays on s (record() reads activations in stream order).
+// stays on s (record() reads activations in stream order); so it does with
+// DMX_SINGLE_STREAM=1 in the environment, which gives per-kernel profiles
+// without overlap.
+bool single_stream_env() {
+    static const bool on = [] {
+        const char *v = std::getenv("DMX_SINGLE_STREAM");
+        return v && v[0] == '1';
+    }();
+    return on;
+}
 struct Branches {
     dmx_runner &r;
     hipStream_t s, t;
     Branches(dmx_runner &runner, hipStream_t main)
-        : r(runner), s(main), t(runner.trace.record || !runner.side ? main : runner.side) {}
+        : r(runner), s(main),
+          t(runner.trace.record || !runner.side || single_stream_env() ? main : runner.side) {}
     void fork() {
         if (t == s) return;
         DMX_HIP(hipEventRecord(r.ev_fork, s));
