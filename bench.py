@@ -8,8 +8,10 @@ stems written to HBM (device entry point dmx_separate_device).
 value = x-realtime = audio seconds / wall seconds over the timed steps.
 
 Also reported: the cross-attention kernel's TFLOP/s at the model's shape
-(Q 2688 vs K/V 1344, 8 heads x 64, batch 8) and its roofline fraction against
-the fp32 MFMA peak, measured with HIP events on the launch stream; and the
+(Q 2688 vs K/V 1344 and Q 1344 vs K/V 2688 in one launch, as the runner
+issues a cross layer's two branches; 8 heads x 64, batch 8) and its roofline
+fraction against the fp32 MFMA peak, measured with HIP events on the launch
+stream; and the
 restated reference CPU backend (oracle/) timed on this host on one 7.8 s
 segment.
 """
@@ -43,35 +45,35 @@ def load_package():
 
 
 def attention_roofline(pkg, torch, batch: int, iters: int):
-    """Average duration of the fused cross-attention kernel at the model's
-    cross shape (Lq = 2688 freq tokens vs Lk = 1344 time tokens, and the
-    reverse direction), timed with events on the stream it is launched on."""
+    """Average duration of the fused cross-attention launch as the runner
+    issues it in the cross layers: both directions of the model's cross shape
+    in one launch (Lq = 2688 spectral tokens vs Lk = 1344 waveform tokens, and
+    Lq = 1344 vs Lk = 2688), timed with events on the stream it is launched on.
+    Returns (ms per launch, algorithmic flops per launch)."""
     from demucs_wgpu_amd import _native
     lib = _native.load()
     heads, D = 8, 512
-    results = []
-    for lq, lk in ((2688, 1344), (1344, 2688)):
-        q = torch.randn(batch, lq, D, device="cuda")
-        k = torch.randn(batch, lk, D, device="cuda")
-        v = torch.randn(batch, lk, D, device="cuda")
-        o = torch.empty(batch, lq, D, device="cuda")
-        stream = torch.cuda.current_stream()
-        sp = ctypes.c_void_p(stream.cuda_stream)
-        args = (sp, ctypes.c_void_p(q.data_ptr()), ctypes.c_void_p(k.data_ptr()), ctypes.c_void_p(v.data_ptr()),
-                ctypes.c_void_p(o.data_ptr()), batch, heads, lq, lk, ctypes.c_float(0.125))
-        for _ in range(3):
-            assert lib.dmx_op_attention(*args) == 0, lib.dmx_last_error()
-        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        start.record(stream)
-        for _ in range(iters):
-            lib.dmx_op_attention(*args)
-        end.record(stream)
-        end.synchronize()
-        ms = start.elapsed_time(end) / iters
-        flops = 4.0 * batch * lq * lk * D  # QK^T + PV, 2 flops per MAC
-        results.append((ms, flops))
-    ms = sum(r[0] for r in results) / len(results)
-    flops = sum(r[1] for r in results) / len(results)
+    (lq0, lk0), (lq1, lk1) = (2688, 1344), (1344, 2688)
+    t = {}
+    for name, lq, lk in (("0", lq0, lk0), ("1", lq1, lk1)):
+        t["q" + name] = torch.randn(batch, lq, D, device="cuda")
+        t["k" + name] = torch.randn(batch, lk, D, device="cuda")
+        t["v" + name] = torch.randn(batch, lk, D, device="cuda")
+        t["o" + name] = torch.empty(batch, lq, D, device="cuda")
+    stream = torch.cuda.current_stream()
+    P = lambda x: ctypes.c_void_p(x.data_ptr())
+    args = (ctypes.c_void_p(stream.cuda_stream), P(t["q0"]), P(t["k0"]), P(t["v0"]), P(t["o0"]), lq0, lk0,
+            P(t["q1"]), P(t["k1"]), P(t["v1"]), P(t["o1"]), lq1, lk1, batch, heads, ctypes.c_float(0.125))
+    for _ in range(3):
+        assert lib.dmx_op_attention_pair(*args) == 0, lib.dmx_last_error()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record(stream)
+    for _ in range(iters):
+        lib.dmx_op_attention_pair(*args)
+    end.record(stream)
+    end.synchronize()
+    ms = start.elapsed_time(end) / iters
+    flops = 4.0 * batch * D * (lq0 * lk0 + lq1 * lk1)  # QK^T + PV, 2 flops per MAC, both problems
     return ms, flops
 
 
@@ -317,7 +319,8 @@ def main():
     roofline = {"bound": "mfma", "achieved": round(attn_tflops, 2), "peak": FP32_MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
                 "frac": round(attn_tflops / FP32_MFMA_PEAK_TFLOPS, 4), "traffic": measured_traffic(),
                 "kernel": "attention_kernel (fused cross-attention, fp32 MFMA)",
-                "per_launch": f"4*B*Lq*Lk*512 flops, B={args.batch_chunks}, (Lq, Lk) = (2688, 1344) and (1344, 2688); "
+                "per_launch": f"sum of 4*B*Lq*Lk*512 flops over (Lq, Lk) = (2688, 1344) and (1344, 2688), "
+                              f"B={args.batch_chunks}, both in one launch as the runner issues them; "
                               f"avg {attn_ms:.3f} ms per launch"}
     line = {
         "metric": "htdemucs x-realtime (audio s / wall s) on 1 MI355X; cross-attn TFLOP/s",

@@ -29,6 +29,7 @@
 //     below 2^ATT_SLACK. O and the row sum carry the same factor, which the
 //     final division cancels.
 #include <type_traits>
+#include <utility>
 
 #include "common.h"
 #include "ops.h"
@@ -53,17 +54,48 @@ constexpr float ATT_SLACK = 8.0f;
 
 __device__ __forceinline__ float4 lds4(const float *p) { return *reinterpret_cast<const float4 *>(p); }
 
+// One launch covers up to two attention problems (the two branches of a
+// transformer layer): blocks [0, p[0].blocks) work on p[0], the rest on p[1].
+// A block is 128 queries of one (batch row, head); within a problem the
+// query blocks of one (row, head) are adjacent, so their K/V stays in L2.
+struct AttProblem {
+    const float *q, *k, *v;
+    float *out;
+    int64_t ldq, ldk, ldv, ldo, q_bs, kv_bs, o_bs;
+    int n_q, n_k, heads, qblocks, blocks;
+};
+struct AttGroup {
+    AttProblem p[2];
+    int count;
+    float scale;
+};
+
+// The problem of this block and its (query block, head, batch row).
+#define DMX_ATT_LOCATE(g)                                                                          \
+    int bid_ = blockIdx.x;                                                                         \
+    const int pi_ = ((g).count > 1 && bid_ >= (g).p[0].blocks) ? 1 : 0;                           \
+    if (pi_) bid_ -= (g).p[0].blocks;                                                              \
+    const AttProblem &P_ = (g).p[pi_];                                                             \
+    const float *__restrict__ q = P_.q;                                                            \
+    const float *__restrict__ k = P_.k;                                                            \
+    const float *__restrict__ v = P_.v;                                                            \
+    float *__restrict__ out = P_.out;                                                              \
+    const int64_t ldq = P_.ldq, ldk = P_.ldk, ldv = P_.ldv, ldo = P_.ldo;                          \
+    const int64_t q_bs = P_.q_bs, kv_bs = P_.kv_bs, o_bs = P_.o_bs;                                \
+    const int n_q = P_.n_q, n_k = P_.n_k;                                                          \
+    const float scale = (g).scale;                                                                 \
+    const int qblock = bid_ % P_.qblocks, head = (bid_ / P_.qblocks) % P_.heads,                  \
+              b = bid_ / (P_.qblocks * P_.heads);
+
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(DMX_ATT_WAVES_PER_EU)))
-void attention_kernel(const float *__restrict__ q, int64_t ldq, const float *__restrict__ k, int64_t ldk,
-                      const float *__restrict__ v, int64_t ldv, float *__restrict__ out, int64_t ldo, int n_q,
-                      int n_k, float scale, int64_t q_bs, int64_t kv_bs, int64_t o_bs) {
+void attention_kernel(const AttGroup g) {
+    DMX_ATT_LOCATE(g)
     __shared__ __align__(16) float Ks[2][ATT_KT][ATT_LD];  // [buffer][key][d]
     __shared__ __align__(16) float Vt[2][ATT_D][ATT_LD];   // [buffer][d][key]
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int head = blockIdx.y, b = blockIdx.z;
     const int j = lane & 31, half = lane >> 5;
-    const int qi = blockIdx.x * (ATT_QW * ATT_WAVES) + wave * ATT_QW + j;
+    const int qi = qblock * (ATT_QW * ATT_WAVES) + wave * ATT_QW + j;
     const bool q_ok = qi < n_q;
 
     const float *qb = q + b * q_bs + head * ATT_D;
@@ -249,18 +281,14 @@ constexpr int ATT_LDV16 = 68;  // bf16 per V^T row (136 B: conflict-free b64 rea
 
 __device__ __forceinline__ bf16x8 to_bf16x8(floatx8 v) { return __builtin_convertvector(v, bf16x8); }
 
-__global__ __launch_bounds__(256) void attention_bf16_kernel(const float *__restrict__ q, int64_t ldq,
-                                                             const float *__restrict__ k, int64_t ldk,
-                                                             const float *__restrict__ v, int64_t ldv,
-                                                             float *__restrict__ out, int64_t ldo, int n_q, int n_k,
-                                                             float scale, int64_t q_bs, int64_t kv_bs, int64_t o_bs) {
+__global__ __launch_bounds__(256) void attention_bf16_kernel(const AttGroup g) {
+    DMX_ATT_LOCATE(g)
     __shared__ __align__(16) __bf16 Ks[2][ATT_KT][ATT_LDK16];  // [buffer][key][d]
     __shared__ __align__(16) __bf16 Vt[2][ATT_D][ATT_LDV16];   // [buffer][d][key]
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int head = blockIdx.y, b = blockIdx.z;
     const int j = lane & 31, half = lane >> 5;
-    const int qi = blockIdx.x * (ATT_QW * ATT_WAVES) + wave * ATT_QW + j;
+    const int qi = qblock * (ATT_QW * ATT_WAVES) + wave * ATT_QW + j;
     const bool q_ok = qi < n_q;
 
     const float *qb = q + b * q_bs + head * ATT_D;
@@ -412,27 +440,64 @@ __global__ __launch_bounds__(256) void attention_bf16_kernel(const float *__rest
 
 }  // namespace
 
+void attention_grouped(hipStream_t s, const AttentionArgs *probs, int count, float scale) {
+    DMX_REQUIRE(count >= 1 && count <= 2, "attention: one or two problems per launch");
+    AttGroup g{};
+    g.count = count;
+    g.scale = scale;
+    int64_t total = 0;
+    // Longer blocks (more keys) first: the tail of the launch is then made of
+    // the short ones.
+    int order[2] = {0, 1};
+    if (count == 2 && probs[1].n_k > probs[0].n_k) std::swap(order[0], order[1]);
+    for (int i = 0; i < count; ++i) {
+        const AttentionArgs &a = probs[order[i]];
+        require_ptrs({a.q, a.k, a.v, a.out}, "attention");
+        DMX_REQUIRE(a.d_head == ATT_D, "attention: only d_head = 64 is implemented");
+        DMX_REQUIRE(a.n_q > 0 && a.n_k > 0 && a.batch > 0 && a.heads > 0, "attention: empty problem");
+        DMX_REQUIRE(a.ldq % 4 == 0 && a.ldk % 4 == 0 && a.ldv % 4 == 0 && a.ldo % 4 == 0 && a.q_batch_stride % 4 == 0 &&
+                        a.kv_batch_stride % 4 == 0 && a.out_batch_stride % 4 == 0,
+                    "attention: row strides must be multiples of 4 floats");
+        DMX_REQUIRE(((reinterpret_cast<uintptr_t>(a.q) | reinterpret_cast<uintptr_t>(a.k) |
+                      reinterpret_cast<uintptr_t>(a.v) | reinterpret_cast<uintptr_t>(a.out)) &
+                     15) == 0,
+                    "attention: operands must be 16-byte aligned");
+        AttProblem &p = g.p[i];
+        p.q = a.q;
+        p.k = a.k;
+        p.v = a.v;
+        p.out = a.out;
+        p.ldq = a.ldq;
+        p.ldk = a.ldk;
+        p.ldv = a.ldv;
+        p.ldo = a.ldo;
+        p.q_bs = a.q_batch_stride;
+        p.kv_bs = a.kv_batch_stride;
+        p.o_bs = a.out_batch_stride;
+        p.n_q = a.n_q;
+        p.n_k = a.n_k;
+        p.heads = a.heads;
+        p.qblocks = (int)ceil_div(a.n_q, ATT_QW * ATT_WAVES);
+        const int64_t blocks = (int64_t)p.qblocks * a.heads * a.batch;
+        DMX_REQUIRE(blocks < (1 << 30), "attention: grid too large");
+        p.blocks = (int)blocks;
+        total += blocks;
+    }
+    DMX_REQUIRE(total < (1ll << 31), "attention: grid too large");
+    const dim3 grid((unsigned)total);
+    if (mfma_precision() == MfmaPrecision::BF16)
+        hipLaunchKernelGGL(attention_bf16_kernel, grid, dim3(256), 0, s, g);
+    else
+        hipLaunchKernelGGL(attention_kernel, grid, dim3(256), 0, s, g);
+    DMX_LAUNCH_CHECK();
+}
+
 void attention(hipStream_t s, const float *q, int64_t ldq, const float *k, int64_t ldk, const float *v, int64_t ldv,
                float *out, int64_t ldo, int batch, int heads, int n_q, int n_k, int d_head, float scale,
                int64_t q_batch_stride, int64_t kv_batch_stride, int64_t out_batch_stride) {
-    require_ptrs({q, k, v, out}, "attention");
-    DMX_REQUIRE(d_head == ATT_D, "attention: only d_head = 64 is implemented");
-    DMX_REQUIRE(n_q > 0 && n_k > 0 && batch > 0 && heads > 0, "attention: empty problem");
-    DMX_REQUIRE(ldq % 4 == 0 && ldk % 4 == 0 && ldv % 4 == 0 && ldo % 4 == 0 && q_batch_stride % 4 == 0 &&
-                    kv_batch_stride % 4 == 0 && out_batch_stride % 4 == 0,
-                "attention: row strides must be multiples of 4 floats");
-    DMX_REQUIRE(((reinterpret_cast<uintptr_t>(q) | reinterpret_cast<uintptr_t>(k) | reinterpret_cast<uintptr_t>(v) |
-                  reinterpret_cast<uintptr_t>(out)) &
-                 15) == 0,
-                "attention: operands must be 16-byte aligned");
-    dim3 grid((unsigned)ceil_div(n_q, ATT_QW * ATT_WAVES), (unsigned)heads, (unsigned)batch);
-    if (mfma_precision() == MfmaPrecision::BF16)
-        hipLaunchKernelGGL(attention_bf16_kernel, grid, dim3(256), 0, s, q, ldq, k, ldk, v, ldv, out, ldo, n_q, n_k,
-                           scale, q_batch_stride, kv_batch_stride, out_batch_stride);
-    else
-        hipLaunchKernelGGL(attention_kernel, grid, dim3(256), 0, s, q, ldq, k, ldk, v, ldv, out, ldo, n_q, n_k, scale,
-                           q_batch_stride, kv_batch_stride, out_batch_stride);
-    DMX_LAUNCH_CHECK();
+    const AttentionArgs a{q,     ldq,   k,   ldk,    v,        ldv,           out,           ldo,
+                          batch, heads, n_q, n_k,    d_head,   q_batch_stride, kv_batch_stride, out_batch_stride};
+    attention_grouped(s, &a, 1, scale);
 }
 
 }  // namespace dmx

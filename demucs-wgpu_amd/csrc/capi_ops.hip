@@ -133,6 +133,18 @@ int dmx_op_attention(void *stream, const float *q, const float *k, const float *
     });
 }
 
+int dmx_op_attention_pair(void *stream, const float *q0, const float *k0, const float *v0, float *out0, int n_q0,
+                          int n_k0, const float *q1, const float *k1, const float *v1, float *out1, int n_q1,
+                          int n_k1, int batch, int heads, float scale) {
+    return guarded([&] {
+        const int64_t D = (int64_t)heads * 64;
+        const AttentionArgs p[2] = {
+            {q0, D, k0, D, v0, D, out0, D, batch, heads, n_q0, n_k0, 64, n_q0 * D, n_k0 * D, n_q0 * D},
+            {q1, D, k1, D, v1, D, out1, D, batch, heads, n_q1, n_k1, 64, n_q1 * D, n_k1 * D, n_q1 * D}};
+        attention_grouped(as_stream(stream), p, 2, scale);
+    });
+}
+
 int dmx_op_layer_norm(void *stream, const float *x, int rows, int dim, const float *w, const float *b, float *out) {
     return guarded([&] { layer_norm_rows(as_stream(stream), x, rows, dim, w, b, out, nullptr, 0); });
 }

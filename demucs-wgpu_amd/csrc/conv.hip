@@ -421,9 +421,19 @@ struct EpLinear {
 // Tile selection
 // ---------------------------------------------------------------------------
 
-// k-tiles in flight in the direct-to-LDS linear kernel (0 = use gemm_kernel).
+// Direct-to-LDS linear kernel: k-tiles in flight (0 = use gemm_kernel), block
+// tile and waves along M.
 #ifndef DMX_DMA_STAGES
-#define DMX_DMA_STAGES 3
+#define DMX_DMA_STAGES 4
+#endif
+#ifndef DMX_DMA_BM
+#define DMX_DMA_BM 128
+#endif
+#ifndef DMX_DMA_BN
+#define DMX_DMA_BN 128
+#endif
+#ifndef DMX_DMA_WM
+#define DMX_DMA_WM 2
 #endif
 
 // Column tile of the 48-channel GLU shapes.
@@ -770,8 +780,8 @@ void linear(hipStream_t s, const float *x, int64_t ldx, int64_t x_batch_stride, 
                         ldx % 4 == 0 && x_batch_stride % 4 == 0;
 #if DMX_DMA_STAGES > 0
     if (dma_ok) {
-        launch_gemm_dma<128, 128, 2, DMX_DMA_STAGES>(s, M, N, K, batches, KMajorRows{x, ldx, x_batch_stride},
-                                                     KMajorRows{w, K, 0}, ep);
+        launch_gemm_dma<DMX_DMA_BM, DMX_DMA_BN, DMX_DMA_WM, DMX_DMA_STAGES>(
+            s, M, N, K, batches, KMajorRows{x, ldx, x_batch_stride}, KMajorRows{w, K, 0}, ep);
         return;
     }
 #else

@@ -424,10 +424,14 @@ __device__ __forceinline__ void lds_wait(floatx4 (&a)[TA], floatx4 (&b)[TB]) {
     pin_regs(a, b);
 }
 
-// Three waves per SIMD (three 4-wave blocks per CU, as the LDS of STAGES = 3
-// allows): registers are capped at 168, which the epilogue must fit too.
+// Waves per SIMD the register allocation leaves room for. Two (four k-tiles
+// in flight, 64 KB of LDS per block) measured 1-3 % faster on the model's
+// linears than three (three k-tiles, registers capped at 168).
+#ifndef DMX_DMA_WPE
+#define DMX_DMA_WPE 2
+#endif
 template <int BM, int BN, int WAVES_M, int STAGES, class EP>
-__global__ __launch_bounds__(GEMM_THREADS) __attribute__((amdgpu_waves_per_eu(3))) void gemm_dma_kernel(int M, int N, int K, KMajorRows al, KMajorRows bl,
+__global__ __launch_bounds__(GEMM_THREADS) __attribute__((amdgpu_waves_per_eu(DMX_DMA_WPE))) void gemm_dma_kernel(int M, int N, int K, KMajorRows al, KMajorRows bl,
                                                                 EP ep) {
     constexpr int BK = 16;                     // two MFMA k-groups of 8 per k-tile
     constexpr int ROWS = BM + BN;              // staged rows per k-tile: A rows, then B rows

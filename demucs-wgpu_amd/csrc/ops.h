@@ -95,6 +95,21 @@ void tokens_to_channels(hipStream_t s, const float *tok, int b, int F, int T, in
 void attention(hipStream_t s, const float *q, int64_t ldq, const float *k, int64_t ldk, const float *v, int64_t ldv,
                float *out, int64_t ldo, int batch, int heads, int n_q, int n_k, int d_head, float scale,
                int64_t q_batch_stride, int64_t kv_batch_stride, int64_t out_batch_stride);
+// Up to two independent problems (same scale) in one launch, e.g. the two
+// branches of a transformer layer; each as the arguments of attention().
+struct AttentionArgs {
+    const float *q;
+    int64_t ldq;
+    const float *k;
+    int64_t ldk;
+    const float *v;
+    int64_t ldv;
+    float *out;
+    int64_t ldo;
+    int batch, heads, n_q, n_k, d_head;
+    int64_t q_batch_stride, kv_batch_stride, out_batch_stride;
+};
+void attention_grouped(hipStream_t s, const AttentionArgs *probs, int count, float scale);
 
 // ---------------- norms / elementwise (norm.cu) ----------------
 void layer_norm_rows(hipStream_t s, const float *x, int rows, int dim, const float *w, const float *b, float *out,

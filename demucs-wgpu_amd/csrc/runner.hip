@@ -347,34 +347,52 @@ void run_dconv(dmx_runner &r, hipStream_t s, float *x, int B, int C, int F, int 
 }
 
 // One `classic_layer_forward` / `cross_layer_forward` (host.rs:1315-1429) on
-// token planes, on stream s; writes the new plane (GroupNorm applied) to out
-// (B, Lq, D). Its temporaries come from s's pool.
-void transformer_layer(dmx_runner &r, hipStream_t s, const TLayerW &L, const float *xq, int64_t Lq, const float *xkv,
-                       int64_t Lk, int B, const std::string &name, float *out) {
-    const int D = r.tch, H = r.hidden, heads = r.cfg.t_heads;
-    const float scale = 1.0f / std::sqrt((float)(D / heads));
+// token planes, in two halves around the attention core so that the two
+// branches' attentions can share one launch.
+//
+// attention_inputs(): LN1 (and LN2 of the key/value plane for a cross layer)
+// and the in-projections, on stream s, into `proj`: a (B, Lq, 3D) q|k|v plane
+// for self-attention, or q (B, Lq, D) followed by k|v (B, Lk, 2D) for cross
+// attention. Returns the attention problem that reads it.
+struct LayerShape {
+    int64_t Lq, Lk;  // Lk = Lq for self-attention
+    int B;
+};
+int64_t projection_floats(const dmx_runner &r, const TLayerW &L, const LayerShape &sh) {
+    const int D = r.tch;
+    return L.cross ? sh.B * sh.Lq * D + sh.B * sh.Lk * 2 * D : sh.B * sh.Lq * 3 * D;
+}
+AttentionArgs attention_inputs(dmx_runner &r, hipStream_t s, const TLayerW &L, const float *xq, const float *xkv,
+                               const LayerShape &sh, float *proj, float *att) {
+    const int D = r.tch, heads = r.cfg.t_heads, B = sh.B;
+    const int64_t Lq = sh.Lq, Lk = sh.Lk;
     DBuf nq = fbuf(s, B * Lq * D);
     layer_norm_rows(s, xq, (int)(B * Lq), D, L.n1w, L.n1b, nq.f(), nullptr, 0);
-    DBuf att = fbuf(s, B * Lq * D);
     if (L.cross) {
         DBuf nk = fbuf(s, B * Lk * D);
         layer_norm_rows(s, xkv, (int)(B * Lk), D, L.n2w, L.n2b, nk.f(), nullptr, 0);
-        DBuf q = fbuf(s, B * Lq * D), kv = fbuf(s, B * Lk * 2 * D);
-        linear(s, nq.f(), D, Lq * D, L.in_w, L.in_b, B, (int)Lq, D, D, q.f(), D, Lq * D, TAIL_BIAS, nullptr, nullptr,
+        float *q = proj, *kv = proj + B * Lq * D;
+        linear(s, nq.f(), D, Lq * D, L.in_w, L.in_b, B, (int)Lq, D, D, q, D, Lq * D, TAIL_BIAS, nullptr, nullptr,
                nullptr);
-        linear(s, nk.f(), D, Lk * D, L.in_w + (int64_t)D * D, L.in_b + D, B, (int)Lk, D, 2 * D, kv.f(), 2 * D,
+        linear(s, nk.f(), D, Lk * D, L.in_w + (int64_t)D * D, L.in_b + D, B, (int)Lk, D, 2 * D, kv, 2 * D,
                Lk * 2 * D, TAIL_BIAS, nullptr, nullptr, nullptr);
-        attention(s, q.f(), D, kv.f(), 2 * D, kv.f() + D, 2 * D, att.f(), D, B, heads, (int)Lq, (int)Lk, D / heads,
-                  scale, Lq * D, Lk * 2 * D, Lq * D);
-    } else {
-        DBuf qkv = fbuf(s, B * Lq * 3 * D);
-        linear(s, nq.f(), D, Lq * D, L.in_w, L.in_b, B, (int)Lq, D, 3 * D, qkv.f(), 3 * D, Lq * 3 * D, TAIL_BIAS,
-               nullptr, nullptr, nullptr);
-        attention(s, qkv.f(), 3 * D, qkv.f() + D, 3 * D, qkv.f() + 2 * D, 3 * D, att.f(), D, B, heads, (int)Lq,
-                  (int)Lq, D / heads, scale, Lq * 3 * D, Lq * 3 * D, Lq * D);
+        return AttentionArgs{q,     D,     kv, 2 * D,    kv + D, 2 * D,      att,        D,
+                             B,     heads, (int)Lq, (int)Lk, D / heads, Lq * D, Lk * 2 * D, Lq * D};
     }
+    linear(s, nq.f(), D, Lq * D, L.in_w, L.in_b, B, (int)Lq, D, 3 * D, proj, 3 * D, Lq * 3 * D, TAIL_BIAS, nullptr,
+           nullptr, nullptr);
+    return AttentionArgs{proj,  3 * D, proj + D, 3 * D,    proj + 2 * D, 3 * D,          att,            D,
+                         B,     heads, (int)Lq,  (int)Lq,  D / heads,    Lq * 3 * D, Lq * 3 * D, Lq * D};
+}
+
+// attention_outputs(): out-projection + LayerScale residual, LN2/LN3, FFN,
+// residual, GroupNorm(1) over the plane, on stream s; writes out (B, Lq, D).
+void attention_outputs(dmx_runner &r, hipStream_t s, const TLayerW &L, const float *xq, const LayerShape &sh,
+                       const float *att, const std::string &name, float *out) {
+    const int D = r.tch, H = r.hidden, B = sh.B;
+    const int64_t Lq = sh.Lq;
     DBuf x1 = fbuf(s, B * Lq * D);
-    linear(s, att.f(), D, Lq * D, L.out_w, L.out_b, B, (int)Lq, D, D, x1.f(), D, Lq * D, TAIL_RESIDUAL_SCALE, xq, L.g1,
+    linear(s, att, D, Lq * D, L.out_w, L.out_b, B, (int)Lq, D, D, x1.f(), D, Lq * D, TAIL_RESIDUAL_SCALE, xq, L.g1,
            nullptr);
     DBuf n2 = fbuf(s, B * Lq * D);
     if (L.cross)
@@ -394,21 +412,35 @@ void transformer_layer(dmx_runner &r, hipStream_t s, const TLayerW &L, const flo
 
 // The layers of the cross-transformer (host.rs:895-941) on the token planes
 // spec (B, Lf, D) and time (B, Lt, D), which are replaced by the outputs.
-// Layer i of the two branches runs concurrently: the waveform layer on the
-// side stream, reading the spectral plane of layer i - 1 (cross layers).
+// Per layer: the two branches' projections run concurrently (waveform on the
+// side stream), both attentions share one launch on s, then the two output
+// halves run concurrently again. Cross layers read the other branch's plane
+// of layer i - 1.
 void transformer_layers(dmx_runner &r, hipStream_t s, DBuf &spec, int64_t Lf, DBuf &time, int64_t Lt, int B) {
-    const int D = r.tch;
+    const int D = r.tch, heads = r.cfg.t_heads;
+    const float scale = 1.0f / std::sqrt((float)(D / heads));
     for (int i = 0; i < r.cfg.t_layers; ++i) {
         std::string n = "crosstransformer.layers." + std::to_string(i);
         std::string nt = "crosstransformer.layers_t." + std::to_string(i);
-        const bool cross = r.layers[i].cross;
+        const TLayerW &Ls = r.layers[i], &Lt_ = r.layers_t[i];
+        const bool cross = Ls.cross;
+        const LayerShape shs{Lf, cross ? Lt : Lf, B}, sht{Lt, cross ? Lf : Lt, B};
+        // Everything both streams touch comes from s's pool, before the fork.
         DBuf ns = fbuf(s, B * Lf * D), nt_ = fbuf(s, (int64_t)B * Lt * D);
+        DBuf ps = fbuf(s, projection_floats(r, Ls, shs)), pt = fbuf(s, projection_floats(r, Lt_, sht));
+        DBuf as = fbuf(s, B * Lf * D), at = fbuf(s, (int64_t)B * Lt * D);
         Branches br(r, s);
         br.fork();
-        transformer_layer(r, br.t, r.layers_t[i], time.f(), Lt, cross ? spec.f() : nullptr, cross ? Lf : 0, B, nt,
-                          nt_.f());
-        transformer_layer(r, s, r.layers[i], spec.f(), Lf, cross ? time.f() : nullptr, cross ? Lt : 0, B, n, ns.f());
+        AttentionArgs prob[2];
+        prob[1] = attention_inputs(r, br.t, Lt_, time.f(), cross ? spec.f() : nullptr, sht, pt.f(), at.f());
+        prob[0] = attention_inputs(r, s, Ls, spec.f(), cross ? time.f() : nullptr, shs, ps.f(), as.f());
         br.join();
+        attention_grouped(s, prob, 2, scale);
+        Branches br2(r, s);
+        br2.fork();
+        attention_outputs(r, br2.t, Lt_, time.f(), sht, at.f(), nt, nt_.f());
+        attention_outputs(r, s, Ls, spec.f(), shs, as.f(), n, ns.f());
+        br2.join();
         spec = std::move(ns);
         time = std::move(nt_);
     }

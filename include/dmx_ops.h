@@ -58,6 +58,13 @@ int dmx_op_pointwise(void *stream, const float *w, const float *bias, const floa
 /* attention_stage (htdemucs.rs:1416-1513) fused: q (B, n_q, H*64), k/v (B, n_k, H*64) -> out (B, n_q, H*64). */
 int dmx_op_attention(void *stream, const float *q, const float *k, const float *v, float *out, int batch, int heads,
                      int n_q, int n_k, float scale);
+/* Two attention problems of the same batch, heads and scale in one launch, as
+ * the runner issues the two branches of each transformer layer (spectral and
+ * waveform tokens). No counterpart in the reference, which dispatches each
+ * branch's attention on its own; it is the launch bench.py's roofline times. */
+int dmx_op_attention_pair(void *stream, const float *q0, const float *k0, const float *v0, float *out0, int n_q0,
+                          int n_k0, const float *q1, const float *k1, const float *v1, float *out1, int n_q1,
+                          int n_k1, int batch, int heads, float scale);
 int dmx_op_layer_norm(void *stream, const float *x, int rows, int dim, const float *w, const float *b, float *out);
 int dmx_op_group_norm(void *stream, const float *x, int b, int c, int inner, int groups, const float *w,
                       const float *bias, float *out);

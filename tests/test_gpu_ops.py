@@ -198,6 +198,31 @@ def test_attention_matches_oracle(lib, oracle, batch, heads, nq, nk):
     assert rms_relative_error(ref, out.cpu().numpy()) < 1e-5
 
 
+@pytest.mark.parametrize("batch,heads,nq0,nk0,nq1,nk1", [(2, 2, 200, 70, 70, 200), (1, 8, 2688, 1344, 1344, 2688),
+                                                        (3, 1, 33, 5, 129, 129)])
+def test_attention_pair_matches_oracle(lib, oracle, batch, heads, nq0, nk0, nq1, nk1):
+    """Two problems in one launch (the blocks of the one with more keys come
+    first): each output matches the oracle on its own problem."""
+    r = rng(nq0 + 7 * nk1)
+    D = heads * 64
+    probs = []
+    for nq, nk in ((nq0, nk0), (nq1, nk1)):
+        q = r.uniform(-2, 2, (batch, nq, D)).astype(np.float32)
+        k = r.uniform(-2, 2, (batch, nk, D)).astype(np.float32)
+        v = r.uniform(-2, 2, (batch, nk, D)).astype(np.float32)
+        ref = np.empty_like(q)
+        for b in range(batch):
+            for h in range(heads):
+                sl = slice(64 * h, 64 * h + 64)
+                ref[b, :, sl] = oracle.attention_head(q[b, :, sl], k[b, :, sl], v[b, :, sl], 0.125)
+        probs.append((dev(q), dev(k), dev(v), torch.empty(q.shape, device="cuda"), ref, nq, nk))
+    (q0, k0, v0, o0, r0, _, _), (q1, k1, v1, o1, r1, _, _) = probs
+    call(lib, "dmx_op_attention_pair", stream(), ptr(q0), ptr(k0), ptr(v0), ptr(o0), nq0, nk0, ptr(q1), ptr(k1),
+         ptr(v1), ptr(o1), nq1, nk1, batch, heads, ctypes.c_float(0.125))
+    assert rms_relative_error(r0, o0.cpu().numpy()) < 1e-5
+    assert rms_relative_error(r1, o1.cpu().numpy()) < 1e-5
+
+
 @pytest.mark.parametrize("ramp", [1.0, 3.0, -3.0])
 def test_attention_running_max_moves_across_tiles(lib, oracle, ramp):
     """Key norms ramp along the sequence, so each query's row max keeps rising
