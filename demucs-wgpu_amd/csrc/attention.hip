@@ -43,6 +43,7 @@ namespace dmx {
 namespace {
 
 typedef float floatx16 __attribute__((ext_vector_type(16)));
+typedef float floatx4 __attribute__((ext_vector_type(4)));
 
 constexpr int ATT_D = 64;
 constexpr int ATT_KT = 64;      // keys per tile
@@ -122,31 +123,29 @@ void attention_kernel(const AttGroup g) {
     // key 16*(s%4) + lane%16, float4 column 4*(s/4) + lane/16 with s = 4*wave + i.
     // A wave then writes 16 keys x 4 columns at once, which keeps the
     // transposed V writes on 64 distinct banks.
-    float4 kpre[4], vpre[4];
+    floatx4 kpre[4], vpre[4];  // vector values: they stay in VGPRs
     auto slot_key = [&](int i) { return 16 * ((4 * wave + i) & 3) + (lane & 15); };
     auto slot_d4 = [&](int i) { return 4 * ((4 * wave + i) >> 2) + (lane >> 4); };
+    // Keys past n_k (ragged last tile) repeat the last key: their scores are
+    // masked to -inf, so those rows never contribute. Branch-free, so the
+    // loads stay ahead of the tile's MFMAs.
     auto fetch = [&](int key0) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            const int kk = key0 + slot_key(i), d = 4 * slot_d4(i);
-            if (kk < n_k) {
-                kpre[i] = *reinterpret_cast<const float4 *>(kb + (int64_t)kk * ldk + d);
-                vpre[i] = *reinterpret_cast<const float4 *>(vb + (int64_t)kk * ldv + d);
-            } else {
-                kpre[i] = make_float4(0.f, 0.f, 0.f, 0.f);
-                vpre[i] = make_float4(0.f, 0.f, 0.f, 0.f);
-            }
+            const int kk = min(key0 + slot_key(i), n_k - 1), d = 4 * slot_d4(i);
+            kpre[i] = *reinterpret_cast<const floatx4 *>(kb + (int64_t)kk * ldk + d);
+            vpre[i] = *reinterpret_cast<const floatx4 *>(vb + (int64_t)kk * ldv + d);
         }
     };
     auto stage = [&](int buf) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const int key = slot_key(i), d = 4 * slot_d4(i);
-            *reinterpret_cast<float4 *>(&Ks[buf][key][d]) = kpre[i];
-            Vt[buf][d + 0][key] = vpre[i].x;
-            Vt[buf][d + 1][key] = vpre[i].y;
-            Vt[buf][d + 2][key] = vpre[i].z;
-            Vt[buf][d + 3][key] = vpre[i].w;
+            *reinterpret_cast<floatx4 *>(&Ks[buf][key][d]) = kpre[i];
+            Vt[buf][d + 0][key] = vpre[i][0];
+            Vt[buf][d + 1][key] = vpre[i][1];
+            Vt[buf][d + 2][key] = vpre[i][2];
+            Vt[buf][d + 3][key] = vpre[i][3];
         }
     };
 
@@ -236,7 +235,11 @@ void attention_kernel(const AttGroup g) {
     for (int t = 0; t < tiles; ++t) {
         const int buf = t & 1;
         const bool more = t + 1 < tiles;
-        if (more) fetch((t + 1) * ATT_KT);
+        // The next tile's loads go out before this tile's MFMAs (on the last
+        // tile they fetch it again, unused): unconditional, and pinned ahead
+        // of the MFMAs by the scheduling barrier.
+        fetch(min(t + 1, tiles - 1) * ATT_KT);
+        __builtin_amdgcn_sched_barrier(0);
         if (!more && ragged)
             tile(std::true_type{}, buf, t * ATT_KT);
         else
@@ -274,7 +277,6 @@ void attention_kernel(const AttGroup g) {
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
 typedef float floatx8 __attribute__((ext_vector_type(8)));
-typedef float floatx4 __attribute__((ext_vector_type(4)));
 
 constexpr int ATT_LDK16 = 72;  // bf16 per K row (144 B: 16-byte aligned, conflict-free b128 reads)
 constexpr int ATT_LDV16 = 68;  // bf16 per V^T row (136 B: conflict-free b64 reads)
@@ -315,17 +317,15 @@ __global__ __launch_bounds__(256) void attention_bf16_kernel(const AttGroup g) {
     float4 kpre[4], vpre[4];
     auto slot_key = [&](int i) { return 16 * ((4 * wave + i) & 3) + (lane & 15); };
     auto slot_d4 = [&](int i) { return 4 * ((4 * wave + i) >> 2) + (lane >> 4); };
+    // Keys past n_k (ragged last tile) repeat the last key: their scores are
+    // masked to -inf, so those rows never contribute. Branch-free, so the
+    // loads stay ahead of the tile's MFMAs.
     auto fetch = [&](int key0) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            const int kk = key0 + slot_key(i), d = 4 * slot_d4(i);
-            if (kk < n_k) {
-                kpre[i] = *reinterpret_cast<const float4 *>(kb + (int64_t)kk * ldk + d);
-                vpre[i] = *reinterpret_cast<const float4 *>(vb + (int64_t)kk * ldv + d);
-            } else {
-                kpre[i] = make_float4(0.f, 0.f, 0.f, 0.f);
-                vpre[i] = make_float4(0.f, 0.f, 0.f, 0.f);
-            }
+            const int kk = min(key0 + slot_key(i), n_k - 1), d = 4 * slot_d4(i);
+            kpre[i] = *reinterpret_cast<const float4 *>(kb + (int64_t)kk * ldk + d);
+            vpre[i] = *reinterpret_cast<const float4 *>(vb + (int64_t)kk * ldv + d);
         }
     };
     auto stage = [&](int buf) {
@@ -415,7 +415,8 @@ __global__ __launch_bounds__(256) void attention_bf16_kernel(const AttGroup g) {
     for (int t = 0; t < tiles; ++t) {
         const int buf = t & 1;
         const bool more = t + 1 < tiles;
-        if (more) fetch((t + 1) * ATT_KT);
+        fetch(min(t + 1, tiles - 1) * ATT_KT);
+        __builtin_amdgcn_sched_barrier(0);
         if (!more && ragged)
             tile(std::true_type{}, buf, t * ATT_KT);
         else
