@@ -36,6 +36,49 @@ __global__ __launch_bounds__(256) void layer_norm_kernel(const float *__restrict
     }
 }
 
+// The same for dim = 4 * 64 * V (the model's 512: V = 2), row held in
+// registers: one read and one write of the row, float4 wide. Same two-pass
+// arithmetic (mean, then the mean of squared deviations).
+template <int V>
+__global__ __launch_bounds__(256) void layer_norm_vec_kernel(const float4 *__restrict__ x, int rows,
+                                                             const float4 *__restrict__ w,
+                                                             const float4 *__restrict__ b, float4 *__restrict__ out,
+                                                             const float4 *__restrict__ add, int add_rows) {
+    constexpr int DIM4 = 64 * V;
+    const int row = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+    if (row >= rows) return;
+    const float4 *xr = x + (int64_t)row * DIM4;
+    float4 v[V];
+#pragma unroll
+    for (int j = 0; j < V; ++j) v[j] = xr[lane + 64 * j];
+    float s = 0.0f;
+#pragma unroll
+    for (int j = 0; j < V; ++j) s += (v[j].x + v[j].y) + (v[j].z + v[j].w);
+    const float mean = wave_sum(s) / (float)(4 * DIM4);
+    float q = 0.0f;
+#pragma unroll
+    for (int j = 0; j < V; ++j) {
+        const float a = v[j].x - mean, c = v[j].y - mean, d = v[j].z - mean, e = v[j].w - mean;
+        q += (a * a + c * c) + (d * d + e * e);
+    }
+    const float var = wave_sum(q) / (float)(4 * DIM4);
+    const float inv = 1.0f / sqrtf(var + 1e-5f);
+    float4 *orow = out + (int64_t)row * DIM4;
+    const float4 *ar = add ? add + (int64_t)(row % add_rows) * DIM4 : nullptr;
+#pragma unroll
+    for (int j = 0; j < V; ++j) {
+        const int i = lane + 64 * j;
+        const float4 wv = w[i], bv = b[i];
+        float4 y = make_float4((v[j].x - mean) * inv * wv.x + bv.x, (v[j].y - mean) * inv * wv.y + bv.y,
+                               (v[j].z - mean) * inv * wv.z + bv.z, (v[j].w - mean) * inv * wv.w + bv.w);
+        if (ar) {
+            const float4 av = ar[i];
+            y = make_float4(y.x + av.x, y.y + av.y, y.z + av.z, y.w + av.w);
+        }
+        orow[i] = y;
+    }
+}
+
 // (b, c, F*T) channel-major -> LayerNorm'd token rows (b, T*F, c), token = t*F + f,
 // plus pos[token] * pos_weight. A block gathers 16 positions x all channels
 // through LDS so both the read and the write are coalesced.
@@ -175,8 +218,18 @@ void layer_norm_rows(hipStream_t s, const float *x, int rows, int dim, const flo
     if (rows <= 0) return;
     require_ptrs({x, w, b, out}, "layer_norm_rows");
     DMX_REQUIRE(!add || add_rows > 0, "layer_norm_rows: add needs a row count");
-    hipLaunchKernelGGL(layer_norm_kernel, dim3((unsigned)ceil_div(rows, 4)), dim3(256), 0, s, x, rows, dim, w, b, out,
-                       add, add ? add_rows : 1);
+    const bool vec = ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(w) | reinterpret_cast<uintptr_t>(b) |
+                       reinterpret_cast<uintptr_t>(out) | reinterpret_cast<uintptr_t>(add)) &
+                      15) == 0;
+    if (vec && dim == 512) {
+        hipLaunchKernelGGL(layer_norm_vec_kernel<2>, dim3((unsigned)ceil_div(rows, 4)), dim3(256), 0, s,
+                           reinterpret_cast<const float4 *>(x), rows, reinterpret_cast<const float4 *>(w),
+                           reinterpret_cast<const float4 *>(b), reinterpret_cast<float4 *>(out),
+                           reinterpret_cast<const float4 *>(add), add ? add_rows : 1);
+    } else {
+        hipLaunchKernelGGL(layer_norm_kernel, dim3((unsigned)ceil_div(rows, 4)), dim3(256), 0, s, x, rows, dim, w, b,
+                           out, add, add ? add_rows : 1);
+    }
     DMX_LAUNCH_CHECK();
 }
 

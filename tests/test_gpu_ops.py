@@ -246,14 +246,15 @@ def test_attention_running_max_moves_across_tiles(lib, oracle, ramp):
     assert rms_relative_error(ref, out.cpu().numpy()) < 1e-5
 
 
-def test_layer_norm_matches_oracle(lib, oracle):
+@pytest.mark.parametrize("rows,dim", [(333, 512), (77, 100)])  # the float4 register path, the generic one
+def test_layer_norm_matches_oracle(lib, oracle, rows, dim):
     r = rng(1)
-    x = r.uniform(-3, 3, (333, 512)).astype(np.float32)
-    w, b = r.uniform(0.5, 1.5, 512).astype(np.float32), r.uniform(-1, 1, 512).astype(np.float32)
+    x = r.uniform(-3, 3, (rows, dim)).astype(np.float32)
+    w, b = r.uniform(0.5, 1.5, dim).astype(np.float32), r.uniform(-1, 1, dim).astype(np.float32)
     ref = oracle.layer_norm(x, w, b)
     out = torch.empty(x.shape, device="cuda")
     dx, dw, db = dev(x), dev(w), dev(b)
-    call(lib, "dmx_op_layer_norm", stream(), ptr(dx), 333, 512, ptr(dw), ptr(db), ptr(out))
+    call(lib, "dmx_op_layer_norm", stream(), ptr(dx), rows, dim, ptr(dw), ptr(db), ptr(out))
     assert rms_relative_error(ref, out.cpu().numpy()) < 1e-6
 
 
