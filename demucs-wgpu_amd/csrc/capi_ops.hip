@@ -105,7 +105,7 @@ int dmx_op_dconv_layer(void *stream, float *x, int B, int C, int F, int T, int d
             st((size_t)4 * B * F * sizeof(double));
         std::unique_ptr<Scratch> keep;
         const float *w1g = gemm_weights(s, w1, hidden, C, 1, 3, keep);
-        dconv_layer(s, x, B, C, F, T, dilation, w1, w1g, b1, hidden, n1w, n1b, w2, b2, n2w, n2b, gamma,
+        dconv_layer(s, x, B, C, F, T, dilation, w1, w1g, nullptr, b1, hidden, n1w, n1b, w2, b2, n2w, n2b, gamma,
                     static_cast<float *>(h.p), static_cast<double *>(st.p));
         DMX_HIP(hipStreamSynchronize(s));
     });

@@ -578,6 +578,11 @@ void conv_dispatch(hipStream_t s, int M, int N, int K, int batches, const KMajor
                            ep);
         return;
     }
+    // A pointwise conv without skip is a plain GEMM over (ic, positions).
+    if (kh == 1 && kw == 1 && sh == 1 && sw == 1 && ph == 0 && pw == 0 && !skip && zdiv == 1 && ow == w) {
+        gemm_auto<GLU>(s, M, N, K, batches, wa, MNMajor{x, (int64_t)ic_stride_h * w, outer}, ep);
+        return;
+    }
 #define DMX_CONV_CASE(A, B)                                                                                \
     if (kh == A && kw == B) {                                                                                \
         gemm_auto<GLU>(s, M, N, K, batches, wa,                                                              \
@@ -707,15 +712,18 @@ void conv_transpose_axis(hipStream_t s, const float *x, int b, int ic, int A, in
 }
 
 void dconv_layer(hipStream_t s, float *x, int B, int C, int F, int T, int dil, const float *w1,
-                 const float *w1_gemm, const float *b1, int H, const float *n1w, const float *n1b, const float *w2,
-                 const float *b2, const float *n2w, const float *n2b, const float *gamma, float *hbuf,
-                 double *stats) {
+                 const float *w1_gemm, const float *w1_t, const float *b1, int H, const float *n1w,
+                 const float *n1b, const float *w2, const float *b2, const float *n2w, const float *n2b,
+                 const float *gamma, float *hbuf, double *stats) {
     require_ptrs({x, w1, w1_gemm, b1, n1w, n1b, w2, b2, n2w, n2b, gamma, hbuf, stats}, "dconv_layer");
     const int rows = B * F;
     DMX_REQUIRE(rows <= 65535, "dconv_layer: too many rows for one launch");
+    if (dconv_narrow_applies(C, H)) {
+        dconv_layer_narrow(s, x, B, C, F, T, dil, w1, w1_t, b1, H, n1w, n1b, w2, b2, n2w, n2b, gamma, hbuf);
+        return;
+    }
     double *st1 = stats, *st2 = stats + 2 * rows;
     zero_doubles(s, stats, 4 * (int64_t)rows);
-    if (dconv_layer_narrow(s, x, B, C, F, T, dil, w1, b1, H, n1w, n1b, w2, b2, n2w, n2b, gamma, hbuf, stats)) return;
     // conv1: k3, dilation dil, padding dil, over t; rows (b, f) as the batch.
     EpConv1 e1;
     e1.y = hbuf;

@@ -314,18 +314,21 @@ __global__ __launch_bounds__(DC_THREADS) void dconv_apply_kernel(float *__restri
 }
 
 template <int C, int H>
-void launch_all(hipStream_t s, float *x, int B, int F, int T, int dil, const float *w1, const float *b1,
-                const float *n1w, const float *n1b, const float *w2, const float *b2, const float *n2w,
-                const float *n2b, const float *gamma, float *hbuf) {
+void launch_all(hipStream_t s, float *x, int B, int F, int T, int dil, const float *w1, const float *w1_t,
+                const float *b1, const float *n1w, const float *n1b, const float *w2, const float *b2,
+                const float *n2w, const float *n2b, const float *gamma, float *hbuf) {
     const int rows = B * F;
     const NarrowScratch sc = carve<C, H>(hbuf, rows, T);
     const int per_row64 = ceil_div(T, C1_POS), per_row_g = ceil_div(T, C1_POS * GR_ITER);
     const int items64 = rows * per_row64, items_g = rows * per_row_g;
-    hipLaunchKernelGGL(dconv_w1_transpose_kernel, dim3((unsigned)ceil_div(H * C * 3, 256)), dim3(256), 0, s, w1, C, H,
-                       sc.w1t);
-    DMX_LAUNCH_CHECK();
+    if (!w1_t) {
+        hipLaunchKernelGGL(dconv_w1_transpose_kernel, dim3((unsigned)ceil_div(H * C * 3, 256)), dim3(256), 0, s, w1, C,
+                           H, sc.w1t);
+        DMX_LAUNCH_CHECK();
+        w1_t = sc.w1t;
+    }
     hipLaunchKernelGGL((dconv_conv1_kernel<C, H>), dim3((unsigned)ceil_div(items64, 4)), dim3(DC_THREADS), 0, s, x, F,
-                       T, dil, per_row64, items64, sc.w1t, b1, sc.y, sc.part1);
+                       T, dil, per_row64, items64, w1_t, b1, sc.y, sc.part1);
     DMX_LAUNCH_CHECK();
     hipLaunchKernelGGL(dconv_gn1_kernel, dim3((unsigned)rows), dim3(DC_THREADS), 0, s, sc.part1, per_row64, H, T, n1w,
                        n1b, sc.aff1);
@@ -353,14 +356,21 @@ int64_t dconv_hidden_floats(int rows, int H, int T) {
            (int64_t)rows * 2 * C * 2 + (int64_t)C * 3 * H;
 }
 
+void dconv_w1_transposed(const float *w1, int C, int H, float *w1_t) {
+    for (int h = 0; h < H; ++h)
+        for (int ck = 0; ck < C * 3; ++ck) w1_t[(int64_t)ck * H + h] = w1[(int64_t)h * C * 3 + ck];
+}
+
+bool dconv_narrow_applies(int C, int H) { return (H == 6 && C == 48) || (H == 12 && C == 96); }
+
 bool dconv_layer_narrow(hipStream_t s, float *x, int B, int C, int F, int T, int dil, const float *w1,
-                        const float *b1, int H, const float *n1w, const float *n1b, const float *w2, const float *b2,
-                        const float *n2w, const float *n2b, const float *gamma, float *hbuf, double *stats) {
-    (void)stats;
+                        const float *w1_t, const float *b1, int H, const float *n1w, const float *n1b,
+                        const float *w2, const float *b2, const float *n2w, const float *n2b, const float *gamma,
+                        float *hbuf) {
     if (H == 6 && C == 48)
-        launch_all<48, 6>(s, x, B, F, T, dil, w1, b1, n1w, n1b, w2, b2, n2w, n2b, gamma, hbuf);
+        launch_all<48, 6>(s, x, B, F, T, dil, w1, w1_t, b1, n1w, n1b, w2, b2, n2w, n2b, gamma, hbuf);
     else if (H == 12 && C == 96)
-        launch_all<96, 12>(s, x, B, F, T, dil, w1, b1, n1w, n1b, w2, b2, n2w, n2b, gamma, hbuf);
+        launch_all<96, 12>(s, x, B, F, T, dil, w1, w1_t, b1, n1w, n1b, w2, b2, n2w, n2b, gamma, hbuf);
     else
         return false;
     return true;

@@ -59,19 +59,24 @@ void pack_conv_transpose(const float *w, int ic, int oc, int k, int st, float *p
 // waveform branch): conv1d k3 dilation `dil` -> GN(1) -> GELU -> 1x1 -> GN(1)
 // -> GLU -> LayerScale -> +residual. `hbuf` holds dconv_hidden_floats()
 // floats, `stats` 4*B*F doubles (both scratch). w1 is the PyTorch (H, C, 3)
-// weight, w1_gemm the same in GEMM order (conv_gemm_weights with kh = 1, kw = 3).
+// weight, w1_gemm the same in GEMM order (conv_gemm_weights with kh = 1,
+// kw = 3), w1_t (may be null) the (C*3, H) transpose the narrow path reads
+// (dconv_w1_transposed; made on the device when null).
 void dconv_layer(hipStream_t s, float *x, int B, int C, int F, int T, int dil, const float *w1,
-                 const float *w1_gemm, const float *b1, int H, const float *n1w, const float *n1b, const float *w2,
-                 const float *b2, const float *n2w, const float *n2b, const float *gamma, float *hbuf,
-                 double *stats);
+                 const float *w1_gemm, const float *w1_t, const float *b1, int H, const float *n1w,
+                 const float *n1b, const float *w2, const float *b2, const float *n2w, const float *n2b,
+                 const float *gamma, float *hbuf, double *stats);
+void dconv_w1_transposed(const float *w1, int C, int H, float *w1_t);
 
 // The same layer with direct VALU kernels for hidden widths where MFMA tiles
 // would be mostly padding (dconv.hip); returns false when it does not apply.
 // Floats of the hidden-activation scratch `hbuf` that dconv_layer needs.
 int64_t dconv_hidden_floats(int rows, int H, int T);
+bool dconv_narrow_applies(int C, int H);
 bool dconv_layer_narrow(hipStream_t s, float *x, int B, int C, int F, int T, int dil, const float *w1,
-                        const float *b1, int H, const float *n1w, const float *n1b, const float *w2, const float *b2,
-                        const float *n2w, const float *n2b, const float *gamma, float *hbuf, double *stats);
+                        const float *w1_t, const float *b1, int H, const float *n1w, const float *n1b,
+                        const float *w2, const float *b2, const float *n2w, const float *n2b, const float *gamma,
+                        float *hbuf);
 
 // out (z, M, N) = W (M, K) . x (z, K, N) + bias[m]  (1x1 conv / channel mixer).
 void pointwise(hipStream_t s, const float *w, const float *bias, const float *x, int batches, int M, int K, int N,

@@ -138,6 +138,7 @@ struct DConvW {
     const float *w1, *b1, *n1w, *n1b, *w2, *b2, *n2w, *n2b, *gamma;
     int hidden;
     const float *w1_gemm;  // w1 in GEMM order (conv_gemm_weights)
+    const float *w1_t;     // w1 as (C*3, H) for the narrow path (dconv_w1_transposed), or null
 };
 
 struct LayerW {
@@ -339,8 +340,8 @@ void run_dconv(dmx_runner &r, hipStream_t s, float *x, int B, int C, int F, int 
         const DConvW &D = L.dconv[d];
         DBuf h = fbuf(s, dconv_hidden_floats(rows, D.hidden, T));
         DBuf st = dbuf(s, 4 * (int64_t)rows);
-        dconv_layer(s, x, B, C, F, T, 1 << d, D.w1, D.w1_gemm, D.b1, D.hidden, D.n1w, D.n1b, D.w2, D.b2, D.n2w, D.n2b,
-                    D.gamma,
+        dconv_layer(s, x, B, C, F, T, 1 << d, D.w1, D.w1_gemm, D.w1_t, D.b1, D.hidden, D.n1w, D.n1b, D.w2, D.b2,
+                    D.n2w, D.n2b, D.gamma,
                     h.f(), st.d());
     }
     (void)r;
@@ -841,10 +842,17 @@ void load_weights(dmx_runner &r, const dmx_tensor *weights, size_t n) {
         for (int d = 0; d < 2; ++d) {
             std::string at = p + ".layers." + std::to_string(d);
             const int hid = ch / hidden_div;
+            const float *w1_t = nullptr;
+            if (dconv_narrow_applies(ch, hid)) {
+                std::vector<float> t((size_t)ch * 3 * hid);
+                dconv_w1_transposed(given[at + ".0.weight"]->data, ch, hid, t.data());
+                w1_t = upload(r, t);
+            }
             L.dconv[d] = {dev(r, at + ".0.weight"), dev(r, at + ".0.bias"), dev(r, at + ".1.weight"),
                           dev(r, at + ".1.bias"),   dev(r, at + ".3.weight"), dev(r, at + ".3.bias"),
                           dev(r, at + ".4.weight"), dev(r, at + ".4.bias"), dev(r, at + ".6.scale"),
-                          hid,                      gemm_order(at + ".0.weight", hid, ch, 1, 3)};
+                          hid,                      gemm_order(at + ".0.weight", hid, ch, 1, 3),
+                          w1_t};
         }
     };
     chin = c.audio_channels;
