@@ -169,9 +169,12 @@ struct dmx_runner {
     int precision = 0;
     hipStream_t stream = nullptr;
     // The waveform branch runs on its own stream beside the spectral one
-    // (both default priority); fork/join are event waits on the GPU.
+    // (all default priority); fork/join are event waits on the GPU.
     hipStream_t side = nullptr;
-    hipEvent_t ev_fork = nullptr, ev_join = nullptr;
+    // A second (main, side) pair: the device separation runs every other
+    // chunk group on it, so two groups' forwards overlap.
+    hipStream_t stream_b = nullptr, side_b = nullptr;
+    hipEvent_t ev_fork = nullptr, ev_join = nullptr, ev_lane = nullptr;
     std::string tag;
     int64_t training_length = 0;
     int hop = 0, pre_channels = 0, tch = 0, hidden = 0, freq_emb_rows = 0;
@@ -244,7 +247,9 @@ struct Branches {
     hipStream_t s, t;
     Branches(dmx_runner &runner, hipStream_t main)
         : r(runner), s(main),
-          t(runner.trace.record || !runner.side || single_stream_env() ? main : runner.side) {}
+          t(runner.trace.record || !runner.side || single_stream_env() ? main
+            : main == runner.stream_b                                   ? runner.side_b
+                                                                        : runner.side) {}
     void fork() {
         if (t == s) return;
         DMX_HIP(hipEventRecord(r.ev_fork, s));
@@ -1054,9 +1059,24 @@ void separate_device(dmx_runner *const *nets, const float *bag_weights, int n_ne
         DBuf acc = fbuf(s, (int64_t)rows * view_len), sum_w = fbuf(s, view_len);
         zero_floats(s, acc.f(), (int64_t)rows * view_len);
         zero_floats(s, sum_w.f(), view_len);
-        DBuf chunk = fbuf(s, (int64_t)group * 2 * seg);
-        DBuf out = fbuf(s, (int64_t)group * rows * seg);
-        DBuf one = bag ? fbuf(s, (int64_t)group * rows * seg) : DBuf();
+        // Chunk groups alternate between two lanes, (stream, side) and
+        // (stream_b, side_b), so the forwards of consecutive groups overlap;
+        // every overlap-add stays on s in group order. A lane's buffers come
+        // from s's pool (taken here, released after the pass) and lane b
+        // waits for s before it reuses them. Progress reports need the
+        // host to wait per group, so they keep one lane.
+        const bool two_lanes = !progress && r0.stream_b && !single_stream_env() && !r0.trace.record;
+        const int lanes = two_lanes ? 2 : 1;
+        std::vector<DBuf> chunk, out, one;
+        for (int l = 0; l < lanes; ++l) {
+            chunk.push_back(fbuf(s, (int64_t)group * 2 * seg));
+            out.push_back(fbuf(s, (int64_t)group * rows * seg));
+            one.push_back(bag ? fbuf(s, (int64_t)group * rows * seg) : DBuf());
+        }
+        // ev_lane marks when lane b's buffers are free: first after the
+        // pass set-up above, then after each of lane b's overlap-adds.
+        if (two_lanes) DMX_HIP(hipEventRecord(r0.ev_lane, s));
+        int lane = 0;
         for (int64_t cursor = 0; cursor < view_len;) {
             std::vector<int64_t> starts, lens;
             while ((int)starts.size() < group && cursor < view_len) {
@@ -1065,24 +1085,33 @@ void separate_device(dmx_runner *const *nets, const float *bag_weights, int n_ne
                 cursor += stride;
             }
             const int g = (int)starts.size();
-            build_chunks(s, mix, samples, stats.d(), g, starts.data(), lens.data(), seg, view_len, offset, mshift,
-                         chunk.f());
+            const hipStream_t ls = lane ? r0.stream_b : s;
+            if (lane) DMX_HIP(hipStreamWaitEvent(ls, r0.ev_lane, 0));
+            float *chunk_p = chunk[lane].f(), *out_p = out[lane].f(), *one_p = one[lane].f();
+            build_chunks(ls, mix, samples, stats.d(), g, starts.data(), lens.data(), seg, view_len, offset, mshift,
+                         chunk_p);
             if (!bag) {
-                forward_device(r0, s, chunk.f(), g, 2, seg, out.f());
+                forward_device(r0, ls, chunk_p, g, 2, seg, out_p);
             } else {
-                zero_floats(s, out.f(), (int64_t)g * rows * seg);
+                zero_floats(ls, out_p, (int64_t)g * rows * seg);
                 for (int n : active) {
-                    forward_device(*nets[n], s, chunk.f(), g, 2, seg, one.f());
-                    bag_accumulate(s, one.f(), g, S, 2 * seg, d_w.f() + n * S, out.f(), 0);
+                    forward_device(*nets[n], ls, chunk_p, g, 2, seg, one_p);
+                    bag_accumulate(ls, one_p, g, S, 2 * seg, d_w.f() + n * S, out_p, 0);
                 }
-                bag_divide(s, out.f(), g, S, 2 * seg, d_tot.f());
+                bag_divide(ls, out_p, g, S, 2 * seg, d_tot.f());
             }
-            ola_accumulate(s, out.f(), g, starts.data(), lens.data(), seg, rows, view_len, weight, acc.f(), sum_w.f());
+            if (lane) {
+                DMX_HIP(hipEventRecord(r0.ev_join, ls));
+                DMX_HIP(hipStreamWaitEvent(s, r0.ev_join, 0));
+            }
+            ola_accumulate(s, out_p, g, starts.data(), lens.data(), seg, rows, view_len, weight, acc.f(), sum_w.f());
+            if (lane) DMX_HIP(hipEventRecord(r0.ev_lane, s));
             done += (size_t)g * active.size();
             if (progress) {
                 DMX_HIP(hipStreamSynchronize(s));
                 progress(done, total, user);
             }
+            lane = (lane + 1) % lanes;
         }
         const int mode = shifts > 1 ? 1 : 0;
         ola_finish(s, acc.f(), sum_w.f(), rows, view_len, trim, samples, stats.d(), scale, mode, stems,
@@ -1171,15 +1200,18 @@ int dmx_runner_create(const dmx_tensor *weights, size_t n_weights, const dmx_con
         r->tag = std::string("hip:") + prop.name + ":" + prop.gcnArchName;
         DMX_HIP(hipStreamCreateWithFlags(&r->stream, hipStreamNonBlocking));
         DMX_HIP(hipStreamCreateWithFlags(&r->side, hipStreamNonBlocking));
+        DMX_HIP(hipStreamCreateWithFlags(&r->stream_b, hipStreamNonBlocking));
+        DMX_HIP(hipStreamCreateWithFlags(&r->side_b, hipStreamNonBlocking));
         DMX_HIP(hipEventCreateWithFlags(&r->ev_fork, hipEventDisableTiming));
         DMX_HIP(hipEventCreateWithFlags(&r->ev_join, hipEventDisableTiming));
+        DMX_HIP(hipEventCreateWithFlags(&r->ev_lane, hipEventDisableTiming));
         load_weights(*r, weights, n_weights);
     });
     if (rc != DMX_OK) {
-        if (r->ev_fork) (void)hipEventDestroy(r->ev_fork);
-        if (r->ev_join) (void)hipEventDestroy(r->ev_join);
-        if (r->side) (void)hipStreamDestroy(r->side);
-        if (r->stream) (void)hipStreamDestroy(r->stream);
+        for (hipEvent_t e : {r->ev_fork, r->ev_join, r->ev_lane})
+            if (e) (void)hipEventDestroy(e);
+        for (hipStream_t st : {r->side, r->stream_b, r->side_b, r->stream})
+            if (st) (void)hipStreamDestroy(st);
         if (r->weight_mem) (void)hipFree(r->weight_mem);
         for (void *p : r->owned) (void)hipFree(p);
         return rc;
@@ -1191,17 +1223,17 @@ int dmx_runner_create(const dmx_tensor *weights, size_t n_weights, const dmx_con
 void dmx_runner_destroy(dmx_runner *r) {
     if (!r) return;
     (void)hipSetDevice(r->device);
-    for (hipStream_t st : {r->stream, r->side})
+    for (hipStream_t st : {r->stream, r->side, r->stream_b, r->side_b})
         if (st) {
             (void)hipStreamSynchronize(st);
             StreamPool::instance().trim(st);
         }
     if (r->weight_mem) (void)hipFree(r->weight_mem);
     for (void *p : r->owned) (void)hipFree(p);
-    if (r->ev_fork) (void)hipEventDestroy(r->ev_fork);
-    if (r->ev_join) (void)hipEventDestroy(r->ev_join);
-    if (r->side) (void)hipStreamDestroy(r->side);
-    if (r->stream) (void)hipStreamDestroy(r->stream);
+    for (hipEvent_t e : {r->ev_fork, r->ev_join, r->ev_lane})
+        if (e) (void)hipEventDestroy(e);
+    for (hipStream_t st : {r->side, r->stream_b, r->side_b, r->stream})
+        if (st) (void)hipStreamDestroy(st);
     delete r;
 }
 
