@@ -67,6 +67,7 @@ SIGNATURES = {
     "dmx_op_conv2d_glu": (_I, [_VP, _VP, _VP] + [_I] * 4 + [_VP, _VP] + [_I] * 5 + [_VP, _F, _VP]),
     "dmx_op_conv_transpose": (_I, [_VP, _VP] + [_I] * 4 + [_VP, _VP] + [_I] * 6 + [_VP]),
     "dmx_op_dconv_layer": (_I, [_VP, _VP] + [_I] * 5 + [_VP, _VP, _I] + [_VP] * 7),
+    "dmx_op_dconv": (_I, [_VP, _VP] + [_I] * 5 + [_VP]),
     "dmx_op_linear": (_I, [_VP, _VP, _I, _I, _VP, _VP, _I, _I, _VP, _VP, _VP]),
     "dmx_op_pointwise": (_I, [_VP, _VP, _VP, _VP, _I, _I, _I, _I, _VP]),
     "dmx_op_attention": (_I, [_VP, _VP, _VP, _VP, _VP, _I, _I, _I, _I, _F]),

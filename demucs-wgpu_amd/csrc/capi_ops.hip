@@ -111,6 +111,41 @@ int dmx_op_dconv_layer(void *stream, float *x, int B, int C, int F, int T, int d
     });
 }
 
+int dmx_op_dconv(void *stream, float *x, int B, int C, int F, int T, int hidden, const float *const *params) {
+    return guarded([&] {
+        hipStream_t s = as_stream(stream);
+        if (!params) throw std::invalid_argument("dmx_op_dconv: params is null");
+        // w1 of each layer as (C*3, H), through the host.
+        std::vector<float> hw((size_t)hidden * C * 3), ht(hw.size());
+        std::unique_ptr<Scratch> w1t[2];
+        DConvRowLayer L[2];
+        DMX_HIP(hipStreamSynchronize(s));
+        for (int d = 0; d < 2; ++d) {
+            const float *const *p = params + 9 * d;
+            require_ptrs({p[0], p[1], p[2], p[3], p[4], p[5], p[6], p[7], p[8]}, "dconv weight");
+            DMX_HIP(hipMemcpy(hw.data(), p[0], hw.size() * sizeof(float), hipMemcpyDeviceToHost));
+            dconv_w1_transposed(hw.data(), C, hidden, ht.data());
+            w1t[d] = std::make_unique<Scratch>(ht.size() * sizeof(float));
+            DMX_HIP(hipMemcpy(w1t[d]->p, ht.data(), ht.size() * sizeof(float), hipMemcpyHostToDevice));
+            L[d] = {static_cast<const float *>(w1t[d]->p), p[1], p[2], p[3], p[4], p[5], p[6], p[7], p[8]};
+        }
+        if (!dconv_rows(s, x, B, C, F, T, hidden, L)) {
+            // Rows too long (or widths the row kernel does not cover): the layers one at a time.
+            Scratch h((size_t)dconv_hidden_floats(B * F, hidden, T) * sizeof(float)),
+                st((size_t)4 * B * F * sizeof(double));
+            for (int d = 0; d < 2; ++d) {
+                const float *const *p = params + 9 * d;
+                std::unique_ptr<Scratch> keep;
+                const float *w1g = gemm_weights(s, p[0], hidden, C, 1, 3, keep);
+                dconv_layer(s, x, B, C, F, T, 1 << d, p[0], w1g, L[d].w1_t, p[1], hidden, p[2], p[3], p[4], p[5],
+                            p[6], p[7], p[8], static_cast<float *>(h.p), static_cast<double *>(st.p));
+                DMX_HIP(hipStreamSynchronize(s));
+            }
+        }
+        DMX_HIP(hipStreamSynchronize(s));
+    });
+}
+
 int dmx_op_linear(void *stream, const float *x, int rows, int K, const float *w, const float *bias, int N, int tail,
                   const float *residual, const float *gamma, float *out) {
     return guarded([&] {

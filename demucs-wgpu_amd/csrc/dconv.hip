@@ -30,6 +30,8 @@
 // Loads read a clamped index unconditionally and are multiplied by a 0/1 mask
 // (a select lets the compiler turn each load into a branch); the data is
 // finite, so the product is exactly the zero padding.
+#include <type_traits>
+
 #include "common.h"
 #include "ops.h"
 
@@ -344,6 +346,310 @@ void launch_all(hipStream_t s, float *x, int B, int F, int T, int dil, const flo
     DMX_LAUNCH_CHECK();
 }
 
+// ---------------------------------------------------------------------------
+// Both DConv layers of a short row in one launch (`dconv_forward`'s loop over
+// depth, host.rs:984-1059): one workgroup per (b, f) row holds the row, C x T,
+// in LDS with a zero halo of RW_PAD positions on each side, runs layer 0
+// (dilation 1) and layer 1 (dilation 2) on it, and writes it back once — x
+// crosses HBM once each way for the two layers, and nothing else does (the
+// hidden activations, their moments and the GN affines stay in LDS).
+//
+// Threads: RW_GROUPS groups of RW_WAVES waves, one position per lane (T <=
+// RW_TMAX). In conv1 group j computes hidden channels [j H/G, (j+1) H/G) of
+// its position, in the apply channels [j C/G, (j+1) C/G); the group index is
+// uniform per wave, so every weight is a scalar load. The moments follow the
+// narrow path above: GN1 from per-thread sums, GN2 from S_h and the Gram
+// matrix of the hidden activations, both reduced in f64.
+constexpr int RW_WAVES = 6;                 // waves per group
+constexpr int RW_TMAX = 64 * RW_WAVES;      // longest row
+constexpr int RW_GROUPS = 2;
+constexpr int RW_THREADS = 64 * RW_WAVES * RW_GROUPS;
+constexpr int RW_PAD = 4;                   // >= the largest dilation (2); keeps rows 16-byte aligned
+constexpr int RW_LDS_BYTES = 160 * 1024;    // gfx950 LDS per workgroup
+
+struct RowLayers {  // kernel argument: both layers' weights
+    DConvRowLayer l[2];
+};
+
+// LDS carve-up, in bytes from the start of the dynamic allocation; every
+// section starts 16-byte aligned.
+template <int C, int H>
+struct RowLds {
+    static constexpr int NS = gram_terms<H>();
+    static constexpr int red = 0;                                  // float [RW_THREADS]
+    static constexpr int sg = red + RW_THREADS * 4;                // double [NS]
+    static constexpr int wsum = sg + ((NS * 8 + 15) / 16) * 16;    // double [2 passes][waves][2]
+    static constexpr int coef = wsum + 2 * (RW_THREADS / 64) * 2 * 8;  // float4 [C]
+    static constexpr int xs = coef + C * 16;                       // float [C][T + 2 PAD]
+    __host__ __device__ static int gs(int T) { return xs + C * (T + 2 * RW_PAD) * 4; }  // float [H][T | 1]
+    __host__ __device__ static int bytes(int T) { return gs(T) + H * (T | 1) * 4; }
+};
+
+// Sum over the wave with DPP moves (no LDS round trips): pairs, quads, half
+// rows and rows by quad_perm / mirrors, then rows 0+1 and 2+3 by row_bcast15
+// and the whole wave by row_bcast31 into lane 63, read from there.
+__device__ __forceinline__ float wave_sum_dpp(float v) {
+    v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0xb1, 0xf, 0xf, false));
+    v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x4e, 0xf, 0xf, false));
+    v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x141, 0xf, 0xf, false));
+    v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x140, 0xf, 0xf, false));
+    v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x142, 0xa, 0xf, false));
+    v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x143, 0xc, 0xf, false));
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
+}
+
+// Sum (a, b) over the workgroup: f32 within each wave (a wave's terms are a
+// few products each), f64 across waves. `buf` holds 2 doubles per wave and
+// must not be reused before the next barrier.
+__device__ __forceinline__ void block_sum2(double &a, double &b, double *buf) {
+    a = wave_sum_dpp((float)a);
+    b = wave_sum_dpp((float)b);
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    if (lane == 0) {
+        buf[2 * wave] = a;
+        buf[2 * wave + 1] = b;
+    }
+    __syncthreads();
+    a = 0.0;
+    b = 0.0;
+#pragma unroll
+    for (int w = 0; w < RW_THREADS / 64; ++w) {
+        a += buf[2 * w];
+        b += buf[2 * w + 1];
+    }
+}
+
+// Row (C, T) between HBM (channel stride cs) and LDS (channel stride S,
+// data from RW_PAD): thread -> (channel offset, V positions), channels
+// advancing by RW_THREADS / (T / V); RW_BATCH channels' loads are issued
+// before the first LDS write (indices clamped, writes guarded).
+constexpr int RW_BATCH = 8;
+template <int C, int V, bool IN>
+__device__ __forceinline__ void row_copy(float *xr, int64_t cs, float *xs, int S, int T) {
+    using vec = typename std::conditional<V == 4, float4, float>::type;
+    const int TV = T / V, cstep = RW_THREADS / TV, c0 = threadIdx.x / TV, tv = (threadIdx.x - c0 * TV) * V;
+    if (c0 >= cstep) return;
+    for (int c = c0; c < C; c += RW_BATCH * cstep) {
+        vec v[RW_BATCH];
+#pragma unroll
+        for (int k = 0; k < RW_BATCH; ++k) {
+            const int cc = min(c + k * cstep, C - 1);
+            v[k] = IN ? *reinterpret_cast<const vec *>(xr + cc * cs + tv)
+                      : *reinterpret_cast<const vec *>(xs + cc * S + RW_PAD + tv);
+        }
+#pragma unroll
+        for (int k = 0; k < RW_BATCH; ++k) {
+            const int cc = c + k * cstep;
+            if (cc < C) {
+                if (IN)
+                    *reinterpret_cast<vec *>(xs + cc * S + RW_PAD + tv) = v[k];
+                else
+                    *reinterpret_cast<vec *>(xr + cc * cs + tv) = v[k];
+            }
+        }
+    }
+}
+
+template <int C, int H>
+__device__ __forceinline__ void row_layer(char *lds, int T, int dil, const DConvRowLayer &L) {
+    using Lay = RowLds<C, H>;
+    constexpr int NS = Lay::NS, HG = H / RW_GROUPS, CG = C / RW_GROUPS;
+    float *red = reinterpret_cast<float *>(lds + Lay::red);
+    double *sg = reinterpret_cast<double *>(lds + Lay::sg);
+    double *wsum = reinterpret_cast<double *>(lds + Lay::wsum);
+    float4 *coef = reinterpret_cast<float4 *>(lds + Lay::coef);
+    float *xs = reinterpret_cast<float *>(lds + Lay::xs);
+    float *gs = reinterpret_cast<float *>(lds + Lay::gs(T));
+    const int S = T + 2 * RW_PAD, TG = T | 1;  // odd hidden-row stride: the Gram pass reads rows at one t
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = uniform(tid >> 6);
+    const int grp = uniform(wave / RW_WAVES);
+    const int t = (wave - grp * RW_WAVES) * 64 + lane;
+    const bool live = t < T;
+    const int tc = min(t, T - 1) + RW_PAD;  // lanes past the row read its last position
+
+    // conv1 (k = 3, dilation dil) for hidden channels [grp HG, grp HG + HG).
+    float acc[HG];
+#pragma unroll
+    for (int j = 0; j < HG; ++j) acc[j] = L.b1[grp * HG + j];
+    {
+        const float *w = L.w1_t + grp * HG;
+        const float *xc = xs + tc;
+#pragma unroll 4
+        for (int c = 0; c < C; ++c, xc += S) {
+            const float x0 = xc[-dil], x1 = xc[0], x2 = xc[dil];
+            const float *wc = w + c * 3 * H;
+#pragma unroll
+            for (int j = 0; j < HG; ++j)
+                acc[j] = fmaf(wc[j], x0, fmaf(wc[H + j], x1, fmaf(wc[2 * H + j], x2, acc[j])));
+        }
+    }
+    // GN1 over (H, T), then GELU, into gs.
+    {
+        double s = 0.0, q = 0.0;
+        if (live) {
+            float fs = 0.0f, fq = 0.0f;
+#pragma unroll
+            for (int j = 0; j < HG; ++j) {
+                fs += acc[j];
+                fq = fmaf(acc[j], acc[j], fq);
+            }
+            s = fs;
+            q = fq;
+        }
+        block_sum2(s, q, wsum);
+        const double m = s / ((double)H * T);
+        const float mean = (float)m, inv = 1.0f / (float)sqrt(fmax(q / ((double)H * T) - m * m, 0.0) + 1e-5);
+        if (live) {
+#pragma unroll
+            for (int j = 0; j < HG; ++j) {
+                const int h = grp * HG + j;
+                const float sc = inv * L.n1w[h];
+                gs[h * TG + t] = gelu(fmaf(acc[j], sc, L.n1b[h] - mean * sc));
+            }
+        }
+    }
+    __syncthreads();
+    // S_h and the upper triangle of G_hh' = sum_t g_h g_h': thread -> (term,
+    // chunk of positions); chunk partials in f32, their sum in f64.
+    {
+        constexpr int J = RW_THREADS / NS;
+        const int i = tid % NS, j = tid / NS;
+        float part = 0.0f;
+        if (j < J) {
+            int ha = i, hb = i;
+            if (i >= H) {  // pair term: walk the triangle rows
+                int k = i - H;
+                ha = 0;
+                while (k >= H - ha) {
+                    k -= H - ha;
+                    ++ha;
+                }
+                hb = ha + k;
+            }
+            const bool sum_term = i < H;
+            const int chunk = (T + J - 1) / J;
+            const int t0 = j * chunk, t1 = min(T, t0 + chunk);
+            const float *ga = gs + ha * TG, *gb = gs + hb * TG;
+            for (int u = t0; u < t1; ++u) part = fmaf(ga[u], sum_term ? 1.0f : gb[u], part);
+        }
+        red[tid] = part;
+        __syncthreads();
+        if (tid < NS) {
+            double a = 0.0;
+            for (int jj = 0; jj < J; ++jj) a += (double)red[jj * NS + tid];
+            sg[tid] = a;
+        }
+        __syncthreads();
+    }
+    // GN2 moments of z_o = W2[o] . g + b2[o] over (2C, T) from S and G; the
+    // GN2 affine per channel, LayerScale folded into the value half.
+    {
+        double sz = 0.0, sz2 = 0.0;
+        const int o = tid;
+        double ws = 0.0;
+        if (o < 2 * C) {
+            double w[H];
+#pragma unroll
+            for (int h = 0; h < H; ++h) w[h] = (double)L.w2[o * H + h];
+            double quad = 0.0;
+            int k = H;
+#pragma unroll
+            for (int h = 0; h < H; ++h) {
+                ws += w[h] * sg[h];
+                quad += w[h] * w[h] * sg[k++];
+#pragma unroll
+                for (int h2 = h + 1; h2 < H; ++h2) quad += 2.0 * w[h] * w[h2] * sg[k++];
+            }
+            const double b = L.b2[o];
+            sz = ws + (double)T * b;
+            sz2 = quad + 2.0 * b * ws + (double)T * b * b;
+        }
+        block_sum2(sz, sz2, wsum + 2 * (RW_THREADS / 64));
+        if (o < 2 * C) {
+            const double cnt = 2.0 * C * (double)T;
+            const double m = sz / cnt;
+            const float mean = (float)m, inv = 1.0f / (float)sqrt(fmax(sz2 / cnt - m * m, 0.0) + 1e-5);
+            const float sc = inv * L.n2w[o], sh = L.n2b[o] + (L.b2[o] - mean) * sc;
+            float2 *cf = reinterpret_cast<float2 *>(coef) + (o < C ? 2 * o : 2 * (o - C) + 1);
+            if (o < C) {
+                const float gm = L.gamma[o];
+                *cf = make_float2(sc * gm, sh * gm);
+            } else {
+                *cf = make_float2(sc, sh);
+            }
+        }
+        __syncthreads();
+    }
+    // z = W2 g, GN2, GLU, LayerScale, += into the row, channels [grp CG, grp CG + CG).
+    if (live) {
+        float g[H];
+#pragma unroll
+        for (int h = 0; h < H; ++h) g[h] = gs[h * TG + t];
+        float *xc = xs + grp * CG * S + t + RW_PAD;
+#pragma unroll 2
+        for (int c = grp * CG; c < grp * CG + CG; ++c, xc += S) {
+            const float *wv = L.w2 + c * H, *wg = L.w2 + (C + c) * H;
+            float v = 0.0f, u = 0.0f;
+#pragma unroll
+            for (int h = 0; h < H; ++h) {
+                v = fmaf(wv[h], g[h], v);
+                u = fmaf(wg[h], g[h], u);
+            }
+            const float4 k = coef[c];
+            *xc = fmaf(fmaf(v, k.x, k.y), fast_sigmoid(fmaf(u, k.z, k.w)), *xc);
+        }
+    }
+    __syncthreads();
+}
+
+// Two workgroups per CU when two rows fit in LDS (C = 48): 6 waves per SIMD.
+template <int C, int H>
+__global__ __launch_bounds__(RW_THREADS) __attribute__((amdgpu_waves_per_eu(C <= 48 ? 6 : 3)))
+void dconv_rows_kernel(float *__restrict__ x, int F, int T, const RowLayers P) {
+    static_assert(H % RW_GROUPS == 0 && C % RW_GROUPS == 0, "groups split H and C evenly");
+    static_assert(2 * C <= RW_THREADS && RowLds<C, H>::NS <= RW_THREADS, "one thread per GN2 channel / term");
+    extern __shared__ __align__(16) char lds[];
+    using Lay = RowLds<C, H>;
+    float *xs = reinterpret_cast<float *>(lds + Lay::xs);
+    const int S = T + 2 * RW_PAD;
+    const int z = blockIdx.x, b = z / F, f = z - b * F;
+    float *xr = x + ((int64_t)b * C * F + f) * T;
+    const int64_t cs = (int64_t)F * T;
+    // Row in, halo zeroed.
+    if ((T & 3) == 0)
+        row_copy<C, 4, true>(xr, cs, xs, S, T);
+    else
+        row_copy<C, 1, true>(xr, cs, xs, S, T);
+    for (int i = threadIdx.x; i < C * 2 * RW_PAD; i += RW_THREADS) {
+        const int c = i / (2 * RW_PAD), e = i - c * 2 * RW_PAD;
+        xs[c * S + (e < RW_PAD ? e : T + e)] = 0.0f;
+    }
+    __syncthreads();
+    row_layer<C, H>(lds, T, 1, P.l[0]);
+    row_layer<C, H>(lds, T, 2, P.l[1]);
+    if ((T & 3) == 0)
+        row_copy<C, 4, false>(xr, cs, xs, S, T);
+    else
+        row_copy<C, 1, false>(xr, cs, xs, S, T);
+}
+
+template <int C, int H>
+bool launch_rows(hipStream_t s, float *x, int B, int F, int T, const RowLayers &P) {
+    const int bytes = RowLds<C, H>::bytes(T);
+    if (T < 1 || T > RW_TMAX || bytes > RW_LDS_BYTES) return false;
+    static const bool lds_ok = hipFuncSetAttribute(reinterpret_cast<const void *>(&dconv_rows_kernel<C, H>),
+                                                   hipFuncAttributeMaxDynamicSharedMemorySize,
+                                                   RW_LDS_BYTES) == hipSuccess;
+    if (!lds_ok) {
+        (void)hipGetLastError();
+        return false;
+    }
+    hipLaunchKernelGGL((dconv_rows_kernel<C, H>), dim3((unsigned)(B * F)), dim3(RW_THREADS), bytes, s, x, F, T, P);
+    DMX_LAUNCH_CHECK();
+    return true;
+}
+
 }  // namespace
 
 int64_t dconv_hidden_floats(int rows, int H, int T) {
@@ -359,6 +665,13 @@ int64_t dconv_hidden_floats(int rows, int H, int T) {
 void dconv_w1_transposed(const float *w1, int C, int H, float *w1_t) {
     for (int h = 0; h < H; ++h)
         for (int ck = 0; ck < C * 3; ++ck) w1_t[(int64_t)ck * H + h] = w1[(int64_t)h * C * 3 + ck];
+}
+
+bool dconv_rows(hipStream_t s, float *x, int B, int C, int F, int T, int H, const DConvRowLayer layers[2]) {
+    const RowLayers P{{layers[0], layers[1]}};
+    if (H == 6 && C == 48) return launch_rows<48, 6>(s, x, B, F, T, P);
+    if (H == 12 && C == 96) return launch_rows<96, 12>(s, x, B, F, T, P);
+    return false;
 }
 
 bool dconv_narrow_applies(int C, int H) { return (H == 6 && C == 48) || (H == 12 && C == 96); }

@@ -73,6 +73,14 @@ void dconv_w1_transposed(const float *w1, int C, int H, float *w1_t);
 // Floats of the hidden-activation scratch `hbuf` that dconv_layer needs.
 int64_t dconv_hidden_floats(int rows, int H, int T);
 bool dconv_narrow_applies(int C, int H);
+// Both layers of a depth-2 DConv (`dconv_forward`, host.rs:984-1059; dilations
+// 1 and 2) in one launch, one workgroup per (b, f) row held in LDS; returns
+// false (nothing launched) unless C = 48 or 96 with H = C/8 and T <= 384.
+// w1_t is each layer's w1 as (C*3, H) (dconv_w1_transposed).
+struct DConvRowLayer {
+    const float *w1_t, *b1, *n1w, *n1b, *w2, *b2, *n2w, *n2b, *gamma;
+};
+bool dconv_rows(hipStream_t s, float *x, int B, int C, int F, int T, int H, const DConvRowLayer layers[2]);
 bool dconv_layer_narrow(hipStream_t s, float *x, int B, int C, int F, int T, int dil, const float *w1,
                         const float *w1_t, const float *b1, int H, const float *n1w, const float *n1b,
                         const float *w2, const float *b2, const float *n2w, const float *n2b, const float *gamma,

@@ -341,6 +341,14 @@ std::vector<float> transition_weight(int64_t n, double power) {
 
 void run_dconv(dmx_runner &r, hipStream_t s, float *x, int B, int C, int F, int T, const LayerW &L) {
     const int rows = B * F;
+    if (L.dconv[0].w1_t && L.dconv[1].w1_t && L.dconv[0].hidden == L.dconv[1].hidden) {
+        DConvRowLayer rl[2];
+        for (int d = 0; d < 2; ++d) {
+            const DConvW &D = L.dconv[d];
+            rl[d] = {D.w1_t, D.b1, D.n1w, D.n1b, D.w2, D.b2, D.n2w, D.n2b, D.gamma};
+        }
+        if (dconv_rows(s, x, B, C, F, T, L.dconv[0].hidden, rl)) return;
+    }
     for (int d = 0; d < 2; ++d) {
         const DConvW &D = L.dconv[d];
         DBuf h = fbuf(s, dconv_hidden_floats(rows, D.hidden, T));

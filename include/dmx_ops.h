@@ -48,6 +48,13 @@ int dmx_op_conv_transpose(void *stream, const float *x, int b, int ic, int A, in
 int dmx_op_dconv_layer(void *stream, float *x, int B, int C, int F, int T, int dilation, const float *w1,
                        const float *b1, int hidden, const float *n1w, const float *n1b, const float *w2,
                        const float *b2, const float *n2w, const float *n2b, const float *gamma);
+/* dconv_forward (crates/demucs-core/src/demucs/host.rs:984-1059): both layers of a
+ * depth-2 DConv (dilations 1 and 2) in place on x (B, C, F, T) whose rows are (b, f).
+ * params holds 18 device pointers, 9 per layer in the order
+ * w1 (H, C, 3), b1, norm1 weight, norm1 bias, w2 (2C, H, 1), b2, norm2 weight,
+ * norm2 bias, LayerScale; H = hidden. Rows of at most 384 positions with
+ * C = 48 or 96 run as one launch with the row in LDS. */
+int dmx_op_dconv(void *stream, float *x, int B, int C, int F, int T, int hidden, const float *const *params);
 /* gemm_into_epilogue (kernels.rs:1531-1621): out (rows, N) = x (rows, K) . W^T + bias
  * with the tail: GELU, or residual + gamma * (.) */
 int dmx_op_linear(void *stream, const float *x, int rows, int K, const float *w, const float *bias, int N, int tail,

@@ -148,10 +148,10 @@ def test_conv_transpose_matches_oracle(lib, oracle, b, ic, A, P, oc, last):
     assert rms_relative_error(ref, out.cpu().numpy()) < 1e-5
 
 
-@pytest.mark.parametrize("B,C,F,T", [(1, 48, 16, 40), (2, 96, 1, 700), (1, 384, 2, 33), (2, 192, 3, 300),
-                                     (1, 48, 1, 1000), (2, 48, 3, 77), (1, 96, 5, 65), (1, 96, 2, 336)])
-def test_dconv_matches_oracle(lib, oracle, dmx, B, C, F, T):
-    r = rng(C + T)
+def dconv_case(C, seed, B, F, T):
+    """Random weights of a depth-2 DConv (PyTorch names under prefix "x") and
+    an input (B, C, F, T), with the oracle's result for it."""
+    r = rng(seed)
     hid = C // 8
     w = {}
     for d in range(2):
@@ -166,8 +166,23 @@ def test_dconv_matches_oracle(lib, oracle, dmx, B, C, F, T):
         w[f"{at}.4.bias"] = r.uniform(-0.2, 0.2, 2 * C).astype(np.float32)
         w[f"{at}.6.scale"] = r.uniform(0.1, 0.5, C).astype(np.float32)
     x = r.uniform(-1, 1, (B, C, F, T)).astype(np.float32)
+    return hid, w, x
+
+
+DCONV_PARAMS = ("0.weight", "0.bias", "1.weight", "1.bias", "3.weight", "3.bias", "4.weight", "4.bias", "6.scale")
+
+
+def dconv_reference(oracle, x, w):
+    B, C, F, T = x.shape
     rows = x.transpose(0, 2, 1, 3).reshape(B * F, C, T)
-    ref = oracle.dconv(rows, w, "x").reshape(B, F, C, T).transpose(0, 2, 1, 3)
+    return oracle.dconv(rows, w, "x").reshape(B, F, C, T).transpose(0, 2, 1, 3)
+
+
+@pytest.mark.parametrize("B,C,F,T", [(1, 48, 16, 40), (2, 96, 1, 700), (1, 384, 2, 33), (2, 192, 3, 300),
+                                     (1, 48, 1, 1000), (2, 48, 3, 77), (1, 96, 5, 65), (1, 96, 2, 336)])
+def test_dconv_matches_oracle(lib, oracle, dmx, B, C, F, T):
+    hid, w, x = dconv_case(C, C + T, B, F, T)
+    ref = dconv_reference(oracle, x, w)
     dx = dev(x)
     dw = {k: dev(v) for k, v in w.items()}
     for d in range(2):
@@ -176,6 +191,22 @@ def test_dconv_matches_oracle(lib, oracle, dmx, B, C, F, T):
              ptr(dw[f"{at}.0.bias"]), hid, ptr(dw[f"{at}.1.weight"]), ptr(dw[f"{at}.1.bias"]),
              ptr(dw[f"{at}.3.weight"]), ptr(dw[f"{at}.3.bias"]), ptr(dw[f"{at}.4.weight"]), ptr(dw[f"{at}.4.bias"]),
              ptr(dw[f"{at}.6.scale"]))
+    assert rms_relative_error(ref, dx.cpu().numpy()) < 1e-5
+
+
+# Rows of up to 384 positions at C = 48 / 96 run both layers in one launch
+# with the row in LDS (T = 336 is the spectral branch's row); the others take
+# the per-layer path behind the same entry point.
+@pytest.mark.parametrize("B,C,F,T", [(2, 96, 4, 336), (1, 48, 8, 336), (1, 48, 16, 40), (3, 48, 2, 1),
+                                     (1, 96, 3, 384), (2, 48, 3, 77), (1, 96, 5, 65), (1, 48, 2, 385),
+                                     (2, 96, 1, 700), (1, 192, 2, 50)])
+def test_dconv_both_layers_matches_oracle(lib, oracle, dmx, B, C, F, T):
+    hid, w, x = dconv_case(C, 7 * C + T, B, F, T)
+    ref = dconv_reference(oracle, x, w)
+    dx = dev(x)
+    dw = [dev(w[f"x.layers.{d}.{name}"]) for d in range(2) for name in DCONV_PARAMS]
+    params = (ctypes.c_void_p * 18)(*[t.data_ptr() for t in dw])
+    call(lib, "dmx_op_dconv", stream(), ptr(dx), B, C, F, T, hid, params)
     assert rms_relative_error(ref, dx.cpu().numpy()) < 1e-5
 
 
