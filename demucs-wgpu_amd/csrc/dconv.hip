@@ -376,13 +376,22 @@ struct RowLayers {  // kernel argument: both layers' weights
 template <int C, int H>
 struct RowLds {
     static constexpr int NS = gram_terms<H>();
+    // Weights in LDS (WL): each layer's W2 (2C, H) in its own section and W1
+    // as [group][c][tap][H / G] (W1P floats per (group, c)) over the hidden
+    // rows, which conv1 does not use; without WL they are scalar loads.
+    static constexpr bool WL = C >= 96;
+    static constexpr int W1P = ((3 * H / RW_GROUPS + 3) / 4) * 4;
     static constexpr int red = 0;                                  // float [RW_THREADS]
     static constexpr int sg = red + RW_THREADS * 4;                // double [NS]
     static constexpr int wsum = sg + ((NS * 8 + 15) / 16) * 16;    // double [2 passes][waves][2]
     static constexpr int coef = wsum + 2 * (RW_THREADS / 64) * 2 * 8;  // float4 [C]
-    static constexpr int xs = coef + C * 16;                       // float [C][T + 2 PAD]
+    static constexpr int w2s = coef + C * 16;                      // float [2C][H] (WL)
+    static constexpr int xs = w2s + (WL ? 2 * C * H * 4 : 0);      // float [C][T + 2 PAD]
     __host__ __device__ static int gs(int T) { return xs + C * (T + 2 * RW_PAD) * 4; }  // float [H][T | 1]
-    __host__ __device__ static int bytes(int T) { return gs(T) + H * (T | 1) * 4; }
+    __host__ __device__ static int bytes(int T) {
+        const int hidden = H * (T | 1) * 4, w1 = WL ? RW_GROUPS * C * W1P * 4 : 0;
+        return gs(T) + (hidden > w1 ? hidden : w1);
+    }
 };
 
 // Sum over the wave with DPP moves (no LDS round trips): pairs, quads, half
@@ -467,12 +476,44 @@ __device__ __forceinline__ void row_layer(char *lds, int T, int dil, const DConv
     const int t = (wave - grp * RW_WAVES) * 64 + lane;
     const bool live = t < T;
     const int tc = min(t, T - 1) + RW_PAD;  // lanes past the row read its last position
+    float *w2s = reinterpret_cast<float *>(lds + Lay::w2s);
+    constexpr int W1P = Lay::W1P;
+
+    if constexpr (Lay::WL) {  // this layer's weights into LDS (the previous layer is done with both regions)
+        for (int i = tid; i < RW_GROUPS * C * 3 * HG; i += RW_THREADS) {
+            const int gc = i / (3 * HG), r = i - gc * (3 * HG), g = gc / C, c = gc - g * C;
+            const int k = r / HG, j = r - k * HG;
+            gs[gc * W1P + r] = L.w1_t[(c * 3 + k) * H + g * HG + j];
+        }
+        for (int i = tid; i < 2 * C * H / 4; i += RW_THREADS)
+            reinterpret_cast<float4 *>(w2s)[i] = reinterpret_cast<const float4 *>(L.w2)[i];
+        __syncthreads();
+    }
 
     // conv1 (k = 3, dilation dil) for hidden channels [grp HG, grp HG + HG).
     float acc[HG];
 #pragma unroll
     for (int j = 0; j < HG; ++j) acc[j] = L.b1[grp * HG + j];
-    {
+    if constexpr (Lay::WL) {
+        const float *xc = xs + tc;
+        const float4 *wq = reinterpret_cast<const float4 *>(gs + grp * C * W1P);
+#pragma unroll 2
+        for (int c = 0; c < C; ++c, xc += S, wq += W1P / 4) {
+            const float x0 = xc[-dil], x1 = xc[0], x2 = xc[dil];
+            float wc[W1P];
+#pragma unroll
+            for (int i = 0; i < W1P / 4; ++i) {
+                const float4 v = wq[i];
+                wc[4 * i] = v.x;
+                wc[4 * i + 1] = v.y;
+                wc[4 * i + 2] = v.z;
+                wc[4 * i + 3] = v.w;
+            }
+#pragma unroll
+            for (int j = 0; j < HG; ++j)
+                acc[j] = fmaf(wc[j], x0, fmaf(wc[HG + j], x1, fmaf(wc[2 * HG + j], x2, acc[j])));
+        }
+    } else {
         const float *w = L.w1_t + grp * HG;
         const float *xc = xs + tc;
 #pragma unroll 4
@@ -587,9 +628,10 @@ __device__ __forceinline__ void row_layer(char *lds, int T, int dil, const DConv
 #pragma unroll
         for (int h = 0; h < H; ++h) g[h] = gs[h * TG + t];
         float *xc = xs + grp * CG * S + t + RW_PAD;
+        const float *w2 = Lay::WL ? w2s : L.w2;
 #pragma unroll 2
         for (int c = grp * CG; c < grp * CG + CG; ++c, xc += S) {
-            const float *wv = L.w2 + c * H, *wg = L.w2 + (C + c) * H;
+            const float *wv = w2 + c * H, *wg = w2 + (C + c) * H;
             float v = 0.0f, u = 0.0f;
 #pragma unroll
             for (int h = 0; h < H; ++h) {
@@ -638,6 +680,8 @@ template <int C, int H>
 bool launch_rows(hipStream_t s, float *x, int B, int F, int T, const RowLayers &P) {
     const int bytes = RowLds<C, H>::bytes(T);
     if (T < 1 || T > RW_TMAX || bytes > RW_LDS_BYTES) return false;
+    if (RowLds<C, H>::WL && ((reinterpret_cast<uintptr_t>(P.l[0].w2) | reinterpret_cast<uintptr_t>(P.l[1].w2)) & 15))
+        return false;  // W2 is copied to LDS as float4
     static const bool lds_ok = hipFuncSetAttribute(reinterpret_cast<const void *>(&dconv_rows_kernel<C, H>),
                                                    hipFuncAttributeMaxDynamicSharedMemorySize,
                                                    RW_LDS_BYTES) == hipSuccess;
