@@ -23,25 +23,108 @@ namespace {
 constexpr int FFT_N = 4096;
 constexpr int FFT_THREADS = 256;
 
-__device__ __forceinline__ unsigned bitrev12(unsigned i) { return __brev(i) >> 20; }
+// 4096-point FFT as three radix-16 Stockham passes (N = 16^3), one thread
+// per 16 points (FFT_N / 16 = FFT_THREADS): pass p takes x[j + 256 r],
+// r < 16, twiddles it by W^(r (j mod Ns) N / (16 Ns)) (Ns = 16^p), runs a
+// 16-point DFT in registers and stores it at (j / Ns) 16 Ns + j mod Ns + r Ns.
+// The first pass reads its inputs from the caller and the last pass leaves
+// x[j + 256 r] = X[j + 256 r] in registers, so only two exchanges go through
+// LDS. W = exp(-2 pi i / N); the inverse (INV) conjugates every twiddle.
+constexpr int FFT_R = 16;
+static_assert(FFT_N == FFT_R * FFT_R * FFT_R && FFT_N / FFT_R == FFT_THREADS, "radix-16 layout");
 
-// In-place radix-2 DIT over buf[FFT_N] already in bit-reversed order.
-// tw[k] = exp(-2 pi i k / N), k < N/2; the inverse conjugates it.
-__device__ void fft4096(float2 *buf, const float2 *__restrict__ tw, bool inverse) {
-    for (int len = 2; len <= FFT_N; len <<= 1) {
-        const int half = len >> 1, step = FFT_N / len;
-        for (int bf = threadIdx.x; bf < FFT_N / 2; bf += FFT_THREADS) {
-            int grp = bf / half, jj = bf - grp * half;
-            int i0 = grp * len + jj, i1 = i0 + half;
-            float2 w = tw[jj * step];
-            if (inverse) w.y = -w.y;
-            float2 a = buf[i0], b = buf[i1];
-            float2 t = make_float2(b.x * w.x - b.y * w.y, b.x * w.y + b.y * w.x);
-            buf[i0] = make_float2(a.x + t.x, a.y + t.y);
-            buf[i1] = make_float2(a.x - t.x, a.y - t.y);
+__device__ __forceinline__ float2 cadd(float2 a, float2 b) { return make_float2(a.x + b.x, a.y + b.y); }
+__device__ __forceinline__ float2 csub(float2 a, float2 b) { return make_float2(a.x - b.x, a.y - b.y); }
+__device__ __forceinline__ float2 cmul(float2 a, float2 b) {
+    return make_float2(a.x * b.x - a.y * b.y, a.x * b.y + a.y * b.x);
+}
+
+// 4-point DFT in place (x0..x3 -> X0..X3); W4 = -i, or +i for the inverse.
+template <bool INV>
+__device__ __forceinline__ void dft4(float2 &a, float2 &b, float2 &c, float2 &d) {
+    const float2 s02 = cadd(a, c), d02 = csub(a, c), s13 = cadd(b, d), d13 = csub(b, d);
+    const float2 rot = INV ? make_float2(-d13.y, d13.x) : make_float2(d13.y, -d13.x);  // W4 * d13
+    a = cadd(s02, s13);
+    c = csub(s02, s13);
+    b = cadd(d02, rot);
+    d = csub(d02, rot);
+}
+
+// 16-point DFT in place, natural order in and out: n = 4 n1 + n2, k = k1 + 4 k2;
+// DFT4 over n1, twiddle W16^(n2 k1), DFT4 over n2, then the 4x4 index transpose.
+template <bool INV>
+__device__ __forceinline__ void dft16(float2 v[16]) {
+    constexpr float C1 = 0.92387953251128674f, S1 = 0.38268343236508977f, R2 = 0.70710678118654752f;
+    const float sg = INV ? 1.0f : -1.0f;  // sign of the twiddles' imaginary parts
+#pragma unroll
+    for (int n2 = 0; n2 < 4; ++n2) dft4<INV>(v[n2], v[4 + n2], v[8 + n2], v[12 + n2]);
+    // v[4 k1 + n2] *= W16^(n2 k1) for n2, k1 in 1..3 (exponents 1, 2, 3, 2, 4, 6, 3, 6, 9).
+    v[5] = cmul(v[5], make_float2(C1, sg * S1));
+    v[6] = cmul(v[6], make_float2(R2, sg * R2));
+    v[7] = cmul(v[7], make_float2(S1, sg * C1));
+    v[9] = cmul(v[9], make_float2(R2, sg * R2));
+    v[10] = make_float2(-sg * v[10].y, sg * v[10].x);  // W16^4 = -i (forward)
+    v[11] = cmul(v[11], make_float2(-R2, sg * R2));
+    v[13] = cmul(v[13], make_float2(S1, sg * C1));
+    v[14] = cmul(v[14], make_float2(-R2, sg * R2));
+    v[15] = cmul(v[15], make_float2(-C1, -sg * S1));
+#pragma unroll
+    for (int k1 = 0; k1 < 4; ++k1) dft4<INV>(v[4 * k1], v[4 * k1 + 1], v[4 * k1 + 2], v[4 * k1 + 3]);
+#pragma unroll
+    for (int a = 0; a < 4; ++a)
+#pragma unroll
+        for (int b = a + 1; b < 4; ++b) {
+            const float2 t = v[4 * a + b];
+            v[4 * a + b] = v[4 * b + a];
+            v[4 * b + a] = t;
         }
-        __syncthreads();
+}
+
+// W^e for 0 <= e < N from the half table tw[k] = W^k, k < N/2 (W^(k + N/2) = -W^k).
+template <bool INV>
+__device__ __forceinline__ float2 twiddle(const float2 *__restrict__ tw, int e) {
+    float2 w = tw[e & (FFT_N / 2 - 1)];
+    if (e & (FFT_N / 2)) w = make_float2(-w.x, -w.y);
+    if (INV) w.y = -w.y;
+    return w;
+}
+
+// LDS index with one float2 of padding per 16 (the first pass stores with a
+// stride of 16 points).
+__device__ __forceinline__ int fft_pad(int i) { return i + (i >> 4); }
+constexpr int FFT_LDS = FFT_N + FFT_N / 16;
+
+// v[r] = x[j + 256 r] on entry, X[j + 256 r] on exit; `buf` is FFT_LDS float2.
+template <bool INV>
+__device__ __forceinline__ void fft4096(float2 v[16], float2 *buf, const float2 *__restrict__ tw) {
+    const int j = threadIdx.x;
+    // pass 0 (Ns = 1): no twiddles; stored at 16 j + r.
+    dft16<INV>(v);
+#pragma unroll
+    for (int r = 0; r < 16; ++r) buf[fft_pad(16 * j + r)] = v[r];
+    __syncthreads();
+    // pass 1 (Ns = 16): twiddle W^(16 r (j mod 16)); stored at (j / 16) 256 + j mod 16 + 16 r.
+#pragma unroll
+    for (int r = 0; r < 16; ++r) v[r] = buf[fft_pad(j + 256 * r)];
+    {
+        const int k = j & 15;
+#pragma unroll
+        for (int r = 1; r < 16; ++r) v[r] = cmul(v[r], twiddle<INV>(tw, 16 * r * k));
     }
+    dft16<INV>(v);
+    __syncthreads();
+    {
+        const int base = (j >> 4) * 256 + (j & 15);
+#pragma unroll
+        for (int r = 0; r < 16; ++r) buf[fft_pad(base + 16 * r)] = v[r];
+    }
+    __syncthreads();
+    // pass 2 (Ns = 256): twiddle W^(r j); the result stays in registers.
+#pragma unroll
+    for (int r = 0; r < 16; ++r) v[r] = buf[fft_pad(j + 256 * r)];
+#pragma unroll
+    for (int r = 1; r < 16; ++r) v[r] = cmul(v[r], twiddle<INV>(tw, r * j));
+    dft16<INV>(v);
 }
 
 // Reflect index of `pad1d_reflect` (spec.rs:204-236) for inputs longer than the pad.
@@ -51,33 +134,44 @@ __device__ __forceinline__ int64_t reflect(int64_t i, int64_t n) {
     return i;
 }
 
-// One kept frame of one (batch, channel) row: frames_out[row][f][bin] (float2),
-// bins 0..N/2-1, scaled by 1/sqrt(N).
+// Two kept frames (f, f + 1) of one (batch, channel) row per block, as the
+// real and imaginary parts of one complex FFT: with z = x1 + i x2,
+// X1[k] = (Z[k] + conj Z[N - k]) / 2 and X2[k] = (Z[k] - conj Z[N - k]) / 2i.
+// frames_out[row][f][bin] (float2), bins 0..N/2-1, scaled by 1/sqrt(N).
 __global__ __launch_bounds__(FFT_THREADS) void stft_kernel(const float *__restrict__ mix, int64_t L, int le,
                                                            const float2 *__restrict__ tw,
                                                            const float *__restrict__ window,
                                                            float2 *__restrict__ frames_out) {
-    __shared__ float2 buf[FFT_N];
-    const int f = blockIdx.x, row = blockIdx.y;
+    __shared__ float2 buf[FFT_LDS];
+    const int f = 2 * blockIdx.x, row = blockIdx.y, j = threadIdx.x;
+    const bool second = f + 1 < le;
     const int hop = FFT_N / 4, pad = hop / 2 * 3;
-    const int64_t padded_len = (int64_t)le * hop + 2 * pad;
     const float *x = mix + (int64_t)row * L;
-    // Frame f + 2 of the centre-padded signal starts at (f + 2) * hop - N/2 in the
-    // reflect-padded one.
-    const int64_t start = (int64_t)(f + 2) * hop - FFT_N / 2;
-    for (int i = threadIdx.x; i < FFT_N; i += FFT_THREADS) {
-        int64_t q = start + i;  // in [0, padded_len)
-        (void)padded_len;
-        int64_t r = reflect(q - pad, L);
-        buf[bitrev12(i)] = make_float2(x[r] * window[i], 0.0f);
+    // Frame f + 2 of the centre-padded signal starts at (f + 2) * hop - N/2 in
+    // the reflect-padded one; every index lies inside the padded signal.
+    const int64_t start = (int64_t)(f + 2) * hop - FFT_N / 2 - pad;
+    float2 v[16];
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+        const int i = j + 256 * r;
+        const float w = window[i];
+        const float a = x[reflect(start + i, L)];
+        const float b = second ? x[reflect(start + hop + i, L)] : 0.0f;
+        v[r] = make_float2(a * w, b * w);
     }
+    fft4096<false>(v, buf, tw);
     __syncthreads();
-    fft4096(buf, tw, false);
-    const float scale = 1.0f / 64.0f;  // 1/sqrt(4096)
-    float2 *dst = frames_out + ((int64_t)row * le + f) * (FFT_N / 2);
-    for (int k = threadIdx.x; k < FFT_N / 2; k += FFT_THREADS) {
-        float2 v = buf[k];
-        dst[k] = make_float2(v.x * scale, v.y * scale);
+#pragma unroll
+    for (int r = 0; r < 16; ++r) buf[fft_pad(j + 256 * r)] = v[r];
+    __syncthreads();
+    const float half_scale = 0.5f / 64.0f;  // the split's 1/2 and 1/sqrt(4096)
+    float2 *d1 = frames_out + ((int64_t)row * le + f) * (FFT_N / 2), *d2 = d1 + FFT_N / 2;
+#pragma unroll
+    for (int r = 0; r < 8; ++r) {
+        const int k = j + 256 * r;
+        const float2 a = v[r], b = buf[fft_pad((FFT_N - k) & (FFT_N - 1))];  // Z[k], Z[N - k]
+        d1[k] = make_float2((a.x + b.x) * half_scale, (a.y - b.y) * half_scale);
+        if (second) d2[k] = make_float2((a.y + b.y) * half_scale, (b.x - a.x) * half_scale);
     }
 }
 
@@ -197,33 +291,51 @@ __global__ __launch_bounds__(256) void ispec_prep_kernel(const float *__restrict
     }
 }
 
-// irfft of one kept frame: Hermitian extension (Nyquist = 0), inverse FFT,
-// real part * (sqrt(N)/N) * window -> frames_out[row][f][0..N).
+// irfft of two kept frames (f, f + 1) per block: Hermitian extensions X1, X2
+// (Nyquist = 0, Im X[0] dropped) packed as Z = X1 + i X2, one inverse FFT, real part -> frame
+// f and imaginary part -> frame f + 1, each * (sqrt(N)/N) * window ->
+// frames_out[row][f][0..N).
 __global__ __launch_bounds__(FFT_THREADS) void irfft_kernel(const float2 *__restrict__ z, int le,
                                                             const float2 *__restrict__ tw,
                                                             const float *__restrict__ window,
                                                             float *__restrict__ frames_out) {
-    __shared__ float2 buf[FFT_N];
-    const int f = blockIdx.x, row = blockIdx.y;
+    __shared__ float2 buf[FFT_LDS];
+    const int f = 2 * blockIdx.x, row = blockIdx.y, j = threadIdx.x;
+    const bool second = f + 1 < le;
     const int bins = FFT_N / 2;
-    const float2 *src = z + ((int64_t)row * le + f) * bins;
-    for (int k = threadIdx.x; k < FFT_N; k += FFT_THREADS) {
-        float2 v;
-        if (k < bins)
-            v = src[k];
-        else if (k == bins)
-            v = make_float2(0.f, 0.f);
-        else {
-            float2 u = src[FFT_N - k];
-            v = make_float2(u.x, -u.y);
+    const float2 *s1 = z + ((int64_t)row * le + f) * bins, *s2 = second ? s1 + bins : s1;
+    float2 v[16];
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+        const int k = j + 256 * r;
+        float2 x1, x2;
+        if (r < 8) {
+            x1 = s1[k];
+            x2 = s2[k];
+            if (k == 0) {  // the real part of the inverse ignores Im X[0]; packed, it would leak across
+                x1.y = 0.0f;
+                x2.y = 0.0f;
+            }
+        } else {  // k >= N/2: conj X[N - k], zero at the Nyquist bin
+            const int m = FFT_N - k;
+            const float nz = k == bins ? 0.0f : 1.0f;
+            const float2 u1 = s1[m & (bins - 1)], u2 = s2[m & (bins - 1)];
+            x1 = make_float2(u1.x * nz, -u1.y * nz);
+            x2 = make_float2(u2.x * nz, -u2.y * nz);
         }
-        buf[bitrev12(k)] = v;
+        if (!second) x2 = make_float2(0.0f, 0.0f);
+        v[r] = make_float2(x1.x - x2.y, x1.y + x2.x);
     }
-    __syncthreads();
-    fft4096(buf, tw, true);
+    fft4096<true>(v, buf, tw);
     const float inv_n = 64.0f / 4096.0f;
-    float *dst = frames_out + ((int64_t)row * le + f) * FFT_N;
-    for (int i = threadIdx.x; i < FFT_N; i += FFT_THREADS) dst[i] = buf[i].x * inv_n * window[i];
+    float *d1 = frames_out + ((int64_t)row * le + f) * FFT_N, *d2 = d1 + FFT_N;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+        const int i = j + 256 * r;
+        const float w = window[i] * inv_n;
+        d1[i] = v[r].x * w;
+        if (second) d2[i] = v[r].y * w;
+    }
 }
 
 // Overlap-add + envelope divide + trim, then out = denorm(time) + wave
@@ -283,7 +395,7 @@ void stft_cac_raw(hipStream_t s, const float *mix, int b, int L, int nfft, float
     DMX_REQUIRE(L > pad + le * hop - L && L > pad, "stft: input shorter than the reflect padding");
     const float2 *tw = reinterpret_cast<const float2 *>(twiddles);
     const float *window = twiddles + nfft;
-    hipLaunchKernelGGL(stft_kernel, dim3((unsigned)le, (unsigned)(b * 2)), dim3(FFT_THREADS), 0, s, mix, (int64_t)L,
+    hipLaunchKernelGGL(stft_kernel, dim3((unsigned)ceil_div(le, 2), (unsigned)(b * 2)), dim3(FFT_THREADS), 0, s, mix, (int64_t)L,
                        le, tw, window, reinterpret_cast<float2 *>(frames_out));
     DMX_LAUNCH_CHECK();
     (void)xspec_out;
@@ -325,7 +437,7 @@ void ispec_and_sum(hipStream_t s, const float *xspec, const float *xtime, int b,
     hipLaunchKernelGGL(ispec_prep_kernel, dim3((unsigned)(bins / 32), (unsigned)ceil_div(le, 32), (unsigned)rows),
                        dim3(256), 0, s, xspec, S, le, norms, z);
     DMX_LAUNCH_CHECK();
-    hipLaunchKernelGGL(irfft_kernel, dim3((unsigned)le, (unsigned)rows), dim3(FFT_THREADS), 0, s, z, le, tw, window,
+    hipLaunchKernelGGL(irfft_kernel, dim3((unsigned)ceil_div(le, 2), (unsigned)rows), dim3(FFT_THREADS), 0, s, z, le, tw, window,
                        frames);
     DMX_LAUNCH_CHECK();
     hipLaunchKernelGGL(ola_sum_kernel, dim3(grid_cap(L, 512), (unsigned)rows), dim3(256), 0, s, frames, le, (int64_t)L,
