@@ -21,17 +21,18 @@ import numpy as np
 
 from . import _native, signals
 from .config import Config
+from .checkpoint import LoadedWeights, config_from_kwargs, load_weights, load_weights_from_bytes
 from .weights import random_init, weight_shapes, xavier_transformer_init
 
 __all__ = [
-    "Backend", "Config", "Demucs", "DmxError", "LoadOptions", "ModelVariant", "Runner", "SeparateOptions",
-    "SeparationProgress", "Stem", "StemId", "StemSelection", "random_init", "weight_shapes",
-    "xavier_transformer_init",
+    "Backend", "Config", "Demucs", "DmxError", "LoadOptions", "LoadedWeights", "ModelVariant", "Runner",
+    "SeparateOptions", "SeparationProgress", "Stem", "StemId", "StemSelection", "config_from_kwargs",
+    "load_weights", "load_weights_from_bytes", "random_init", "weight_shapes", "xavier_transformer_init",
 ]
 
 # dmx_status -> reference Error variant (crates/demucs-core/src/error.rs:4-55)
 STATUS_NAMES = {1: "Shape", 2: "Config", 3: "MissingWeight", 4: "WeightShape", 5: "UnsupportedModel", 6: "Gpu",
-                7: "Memory", 8: "Argument"}
+                7: "Memory", 8: "Argument", 9: "Checkpoint", 10: "Io"}
 PRECISION_FP32, PRECISION_BF16 = 0, 1
 
 
@@ -293,14 +294,24 @@ class Demucs:
     @classmethod
     def load(cls, weights, opts: Optional[LoadOptions] = None, backend: Optional[Backend] = None,
              config: Optional[Config] = None, bag_weights: Optional[np.ndarray] = None) -> "Demucs":
-        """`weights` is one name -> array mapping, or a list of them for the bag
-        (with `bag_weights` (networks x sources), identity by default)."""
+        """`weights` is one network or a list of them for the bag (with
+        `bag_weights` (networks x sources), identity by default). A network is
+        a name -> array mapping, a `LoadedWeights`, or a checkpoint path
+        (`load_weights`: torch zip or safetensors); the config of a loaded
+        checkpoint is used unless `config` is given."""
         opts = opts or LoadOptions()
         backend = backend or Backend.auto()
         if backend.kind == "cpu":
             raise DmxError(5, "the CPU backend is the reference's own host path; this package provides Backend.hip")
         nets = weights if isinstance(weights, (list, tuple)) else [weights]
-        runners = [Runner(w, config, backend.device) for w in nets]
+        runners = []
+        for w in nets:
+            if isinstance(w, (str, bytes)) or hasattr(w, "__fspath__"):
+                w = load_weights(w)
+            if isinstance(w, LoadedWeights):
+                runners.append(Runner(w.tensors, config or w.config, backend.device))
+            else:
+                runners.append(Runner(w, config, backend.device))
         if len(runners) > 1 and bag_weights is None:
             bag_weights = np.eye(len(runners), runners[0].config.sources, dtype=np.float32)
         return cls(runners, bag_weights, opts)

@@ -1,4 +1,4 @@
-"""ctypes binding of libdmx.so (include/dmx.h, include/dmx_ops.h).
+"""ctypes binding of libdmx.so (include/dmx.h, include/dmx_ops.h, include/dmx_ckpt.h).
 
 The library is built in-tree by ``build.py`` (hipcc, gfx950). Loading fails
 loudly when it is missing: there is no fallback implementation.
@@ -40,8 +40,8 @@ class CSeparateOptions(ctypes.Structure):
     ]
 
 
-# name -> (restype, argtypes). Every symbol declared in include/dmx.h and
-# include/dmx_ops.h appears here; tests check the library exports them all.
+# name -> (restype, argtypes). Every function declared in include/*.h appears
+# here; tests check the library exports them all.
 _VP, _I, _I64, _F, _D, _SZ = ctypes.c_void_p, ctypes.c_int, ctypes.c_int64, ctypes.c_float, ctypes.c_double, ctypes.c_size_t
 SIGNATURES = {
     "dmx_config_default": (None, [_VP]),
@@ -79,6 +79,17 @@ SIGNATURES = {
     "dmx_op_set_precision": (_I, [_I]),
     "dmx_op_spec_normalise": (_I, [_VP, _VP, _I, _I, _VP, _VP, _VP]),
     "dmx_op_ispec_sum": (_I, [_VP, _VP, _VP, _I, _I, _VP, _VP]),
+    # include/dmx_ckpt.h
+    "dmx_checkpoint_load": (_I, [ctypes.c_char_p, ctypes.POINTER(_VP)]),
+    "dmx_checkpoint_from_bytes": (_I, [_VP, _SZ, _I, ctypes.POINTER(_VP)]),
+    "dmx_checkpoint_free": (None, [_VP]),
+    "dmx_checkpoint_count": (_SZ, [_VP]),
+    "dmx_checkpoint_tensors": (ctypes.POINTER(CTensor), [_VP]),
+    "dmx_checkpoint_metadata": (ctypes.c_char_p, [_VP, ctypes.c_char_p]),
+    "dmx_checkpoint_metadata_count": (_SZ, [_VP]),
+    "dmx_checkpoint_metadata_key": (ctypes.c_char_p, [_VP, _SZ]),
+    "dmx_checkpoint_config": (_I, [_VP, _VP]),
+    "dmx_config_from_kwargs": (_I, [ctypes.c_char_p, _VP]),
 }
 
 _lib = None

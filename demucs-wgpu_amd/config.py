@@ -69,3 +69,7 @@ class Config:
 
     def to_c(self) -> CConfig:
         return CConfig(**{f.name: getattr(self, f.name) for f in fields(self)})
+
+    @classmethod
+    def from_c(cls, c: CConfig) -> "Config":
+        return cls(**{f.name: getattr(c, f.name) for f in fields(cls)})

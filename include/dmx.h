@@ -34,7 +34,9 @@ enum dmx_status {
     DMX_ERR_UNSUPPORTED = 5,    /* Error::UnsupportedModel */
     DMX_ERR_GPU = 6,            /* Error::Gpu */
     DMX_ERR_MEMORY = 7,         /* Error::Memory */
-    DMX_ERR_ARGUMENT = 8        /* null pointer / bad enum at the C boundary */
+    DMX_ERR_ARGUMENT = 8,       /* null pointer / bad enum at the C boundary */
+    DMX_ERR_CHECKPOINT = 9,     /* Error::Checkpoint / Error::Pickle (dmx_ckpt.h) */
+    DMX_ERR_IO = 10             /* Error::Io (dmx_ckpt.h) */
 };
 
 enum dmx_precision {

@@ -3,8 +3,13 @@
 and random-init weights; plus the SegmentForward contract (two groups in
 flight, batch independence) and the error paths the C-ABI must raise.
 """
+import dataclasses
+import json
+
 import numpy as np
 import pytest
+import torch
+from safetensors.numpy import save as st_save
 
 from conftest import small_config, snr_db
 
@@ -242,3 +247,29 @@ def test_bf16_separation_meets_the_40_db_gate(dmx, oracle, small):
     out = dmx.separate_runners([runner], mix[0], mix[1], 44100, opts)
     for s in range(4):
         assert snr_db(ref[s], out[s]) >= 40.0, (s, snr_db(ref[s], out[s]))
+
+
+@pytest.mark.parametrize("container", ["safetensors", "th"])
+def test_a_checkpoint_file_loads_into_the_device_forward(dmx, oracle, small, tmp_path, container):
+    """`Demucs.load(path)`: weights stored as F16 (as the published checkpoints
+    are) come back widened to f32, the safetensors kwargs give the config, and
+    the forward matches the oracle run on the same widened weights."""
+    cfg, weights, _, _ = small
+    w16 = {k: v.astype(np.float16) for k, v in weights.items()}
+    if container == "safetensors":
+        path = tmp_path / "net.safetensors"
+        kwargs = dataclasses.asdict(cfg)
+        kwargs["sources"] = list(dmx.Config.SOURCES)
+        kwargs["cac"] = bool(kwargs["cac"])
+        path.write_bytes(st_save(w16, metadata={"kwargs": json.dumps(kwargs)}))
+        net = dmx.Demucs.load(str(path))
+    else:
+        path = tmp_path / "net.th"
+        torch.save({"klass": None, "kwargs": {}, "state": {k: torch.from_numpy(v) for k, v in w16.items()}}, path)
+        net = dmx.Demucs.load(path, config=cfg)
+    assert net.runners[0].config == cfg
+    mix = dmx.signals.gaussian_segments(4, 1, cfg.training_length)
+    out = net.forward_segment(mix)
+    ref = oracle.Model({k: v.astype(np.float32) for k, v in w16.items()}, cfg).forward(mix)
+    snrs = per_stem_snr(ref, out)
+    assert min(snrs) >= 60.0, snrs
