@@ -468,10 +468,22 @@ void gemm_pick(hipStream_t s, int M, int N, int K, int batches, const AL &al, co
             launch_gemm<96, 128, 1, false, BF16>(s, M, N, K, batches, al, bl, ep);
         else if (M >= 96)
             launch_gemm<128, 128, 2, false, BF16>(s, M, N, K, batches, al, bl, ep);
-        else if (M > 32)
-            launch_gemm<64, 128, 2, false, BF16>(s, M, N, K, batches, al, bl, ep);
-        else
-            launch_gemm<32, 256, 1, false, BF16>(s, M, N, K, batches, al, bl, ep);
+        else if (M > 32) {
+            // 64-row tiles: 64-wide columns when 128-wide ones would leave CUs idle.
+            if (ceil_div(N, 128) * ceil_div(M, 64) * batches < 256)
+                launch_gemm<64, 64, 2, false, BF16>(s, M, N, K, batches, al, bl, ep);
+            else
+                launch_gemm<64, 128, 2, false, BF16>(s, M, N, K, batches, al, bl, ep);
+        } else {
+            // 32-row tiles: 128-wide columns unless 256-wide ones fill two rounds
+            // of the CUs with little padding (short rows such as T = 336 pad a
+            // 256-wide tile by a third).
+            const int64_t n256 = ceil_div(N, 256) * 256;
+            if (ceil_div(N, 256) * batches >= 512 && 5 * n256 <= 6 * (int64_t)N)
+                launch_gemm<32, 256, 1, false, BF16>(s, M, N, K, batches, al, bl, ep);
+            else
+                launch_gemm<32, 128, 1, false, BF16>(s, M, N, K, batches, al, bl, ep);
+        }
     }
 }
 
