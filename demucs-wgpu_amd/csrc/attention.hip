@@ -71,12 +71,30 @@ struct AttGroup {
     float scale;
 };
 
+// Within a problem whose (row, head) pairs split evenly over the 8 XCDs (and
+// which starts on XCD 0), XCD x runs all query blocks of pairs x, x + 8, ...:
+// a pair's K/V is then read into one L2, and every XCD gets the same share of
+// each problem, long-key blocks first.
+__device__ __forceinline__ int att_xcd_block(int bid, const AttProblem &P, bool aligned) {
+#if DMX_XCD_REMAP
+    const int pairs = P.blocks / P.qblocks;
+    if (!aligned || pairs % XCDS != 0) return bid;
+    const int x = bid % XCDS, local = bid / XCDS;
+    return ((local / P.qblocks) * XCDS + x) * P.qblocks + local % P.qblocks;
+#else
+    (void)P;
+    (void)aligned;
+    return bid;
+#endif
+}
+
 // The problem of this block and its (query block, head, batch row).
 #define DMX_ATT_LOCATE(g)                                                                          \
     int bid_ = blockIdx.x;                                                                         \
     const int pi_ = ((g).count > 1 && bid_ >= (g).p[0].blocks) ? 1 : 0;                           \
     if (pi_) bid_ -= (g).p[0].blocks;                                                              \
     const AttProblem &P_ = (g).p[pi_];                                                             \
+    bid_ = att_xcd_block(bid_, P_, pi_ == 0 || (g).p[0].blocks % XCDS == 0);                       \
     const float *__restrict__ q = P_.q;                                                            \
     const float *__restrict__ k = P_.k;                                                            \
     const float *__restrict__ v = P_.v;                                                            \

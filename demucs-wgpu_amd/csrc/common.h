@@ -114,6 +114,25 @@ __device__ __forceinline__ float gelu(float x) { return 0.5f * x * (1.0f + erf_n
 // Logistic sigmoid with the hardware reciprocal and exponential.
 __device__ __forceinline__ float sigmoid(float g) { return __builtin_amdgcn_rcpf(1.0f + fast_exp(-g)); }
 
+// Workgroup placement across the 8 XCDs (each with its own L2): blocks are
+// handed out round-robin, block i to XCD i % 8. xcd_contiguous() maps the
+// launch index to a logical block so that each XCD runs one contiguous range
+// of the logical order (sizes differ by at most one), which keeps blocks that
+// share operand panels on one L2. DMX_XCD_REMAP=0 keeps the launch order.
+#ifndef DMX_XCD_REMAP
+#define DMX_XCD_REMAP 1
+#endif
+constexpr int XCDS = 8;
+__device__ __forceinline__ int xcd_contiguous(int bid, int total) {
+#if DMX_XCD_REMAP
+    const int x = bid % XCDS, local = bid / XCDS, q = total / XCDS, r = total % XCDS;
+    return x < r ? x * (q + 1) + local : r * (q + 1) + (x - r) * q + local;
+#else
+    (void)total;
+    return bid;
+#endif
+}
+
 // Wave64 reductions.
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll

@@ -112,6 +112,16 @@ struct KMajorRows {
     __device__ const float *row(int z, int r) const { return p + z * batch_stride + (int64_t)r * ld; }
 };
 
+// This block's (column tile, row tile, batch) in the XCD-contiguous order of
+// the x-fastest grid: an XCD runs consecutive column tiles of one row panel.
+__device__ __forceinline__ void block_tile(int &bx, int &by, int &z) {
+    const int nx = gridDim.x, ny = gridDim.y;
+    const int lb = xcd_contiguous(blockIdx.x + nx * (blockIdx.y + ny * blockIdx.z), nx * ny * gridDim.z);
+    bx = lb % nx;
+    by = (lb / nx) % ny;
+    z = lb / (nx * ny);
+}
+
 template <int BM, int BN, int WAVES_M, bool GLU, bool BF16, class AL, class BL, class EP>
 __global__ __launch_bounds__(GEMM_THREADS) void gemm_kernel(int M, int N, int K, AL al, BL bl, EP ep) {
     using T = typename GemmStage<BF16>::T;
@@ -130,9 +140,10 @@ __global__ __launch_bounds__(GEMM_THREADS) void gemm_kernel(int M, int N, int K,
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int wm = wave % WAVES_M, wn = wave / WAVES_M;
-    const int z = blockIdx.z;
-    const int n0 = blockIdx.x * BN;
-    const int m_block = blockIdx.y * (GLU ? BM / 2 : BM);
+    int bx, by, z;
+    block_tile(bx, by, z);
+    const int n0 = bx * BN;
+    const int m_block = by * (GLU ? BM / 2 : BM);
     ep.init(z);
 
     // Logical tile row -> physical A row (-1 when out of range).
@@ -448,8 +459,9 @@ __global__ __launch_bounds__(GEMM_THREADS) __attribute__((amdgpu_waves_per_eu(DM
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int wm = wave % WAVES_M, wn = wave / WAVES_M;
-    const int z = blockIdx.z;
-    const int n0 = blockIdx.x * BN, m0 = blockIdx.y * BM;
+    int bx, by, z;
+    block_tile(bx, by, z);
+    const int n0 = bx * BN, m0 = by * BM;
     ep.init(z);
 
     // Sources of this lane's DMA slots. Rows past M / N repeat the last row:
