@@ -71,6 +71,20 @@ int dmx_op_conv2d_glu(void *stream, const float *x, const float *skip, int b, in
                       float emb_scale, float *out) {
     return guarded([&] {
         hipStream_t s = as_stream(stream);
+        if (kh == 3 && kw == 3 && ph == 1 && pw == 1 && !emb && winograd_applies(ic, C, h, w)) {
+            // The decoder rewrite's shape: the Winograd path the runner takes for it.
+            require_ptrs({x, weight, bias, out}, "conv2d_glu");
+            std::vector<float> hw((size_t)2 * C * ic * 9), u((size_t)16 * 2 * C * ic);
+            DMX_HIP(hipStreamSynchronize(s));
+            DMX_HIP(hipMemcpy(hw.data(), weight, hw.size() * sizeof(float), hipMemcpyDeviceToHost));
+            winograd_weights(hw.data(), 2 * C, ic, u.data());
+            Scratch du(u.size() * sizeof(float)), ws((size_t)winograd_scratch_floats(b, ic, C, h, w) * sizeof(float));
+            DMX_HIP(hipMemcpy(du.p, u.data(), u.size() * sizeof(float), hipMemcpyHostToDevice));
+            conv3x3_glu_winograd(s, x, skip, b, ic, C, h, w, static_cast<const float *>(du.p), bias, out,
+                                 static_cast<float *>(ws.p));
+            DMX_HIP(hipStreamSynchronize(s));
+            return;
+        }
         std::unique_ptr<Scratch> keep;
         const float *wg = gemm_weights(s, weight, 2 * C, ic, kh, kw, keep);
         conv2d_glu(s, x, skip, b, ic, h, w, wg, bias, C, kh, kw, ph, pw, out, emb, emb_scale);

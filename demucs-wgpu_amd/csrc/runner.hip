@@ -143,6 +143,7 @@ struct DConvW {
 
 struct LayerW {
     const float *conv_w = nullptr, *conv_b = nullptr, *rw = nullptr, *rb = nullptr;
+    const float *rw_wino = nullptr;  // decoder rewrite as Winograd U (winograd_weights), or null
     int cin = 0, cout = 0;
     DConvW dconv[2];
 };
@@ -646,7 +647,12 @@ void forward_full(dmx_runner &r, hipStream_t s, const float *mix, int B, float *
         DBuf skip = std::move(saved.back());
         saved.pop_back();
         DBuf g = fbuf(s, (int64_t)B * cin * F * le);
-        conv2d_glu(s, x.f(), skip.f(), B, cin, F, le, FL.rw, FL.rb, cin, 3, 3, 1, 1, g.f(), nullptr, 0.f);
+        if (FL.rw_wino && winograd_applies(cin, cin, F, le)) {
+            DBuf ws = fbuf(s, winograd_scratch_floats(B, cin, cin, F, le));
+            conv3x3_glu_winograd(s, x.f(), skip.f(), B, cin, cin, F, le, FL.rw_wino, FL.rb, g.f(), ws.f());
+        } else {
+            conv2d_glu(s, x.f(), skip.f(), B, cin, F, le, FL.rw, FL.rb, cin, 3, 3, 1, 1, g.f(), nullptr, 0.f);
+        }
         skip.release();
         run_dconv(r, s, g.f(), B, cin, F, le, FL);
         record(r, "decoder." + std::to_string(i) + "#1", g.f(), {B, cin, F, le});
@@ -906,6 +912,11 @@ void load_weights(dmx_runner &r, const dmx_tensor *weights, size_t n) {
         L.conv_b = dev(r, d + ".conv_tr.bias");
         L.rw = gemm_order(d + ".rewrite.weight", 2 * L.cin, L.cin, 3, 3);
         L.rb = dev(r, d + ".rewrite.bias");
+        if (winograd_channels(L.cin, L.cin)) {
+            std::vector<float> u((size_t)16 * 2 * L.cin * L.cin);
+            winograd_weights(given[d + ".rewrite.weight"]->data, 2 * L.cin, L.cin, u.data());
+            L.rw_wino = upload(r, u);
+        }
         fill_dconv(L, d + ".dconv", L.cin);
         r.dec.push_back(L);
         LayerW T;

@@ -114,6 +114,26 @@ def test_conv2d_glu_matches_oracle(lib, oracle, b, ic, h, w, C, kh, kw):
     assert rms_relative_error(ref, out.cpu().numpy()) < 1e-5
 
 
+# 3x3 / padding 1 with at least 192 output channels: the decoder rewrite's
+# shape, which runs as Winograd F(2x2, 3x3) (input transform, 16 batched GEMMs,
+# output transform + GLU); odd sizes leave partial 2x2 tiles at the edges.
+@pytest.mark.parametrize("b,ic,h,w,C,with_skip", [(2, 192, 8, 20, 192, True), (1, 384, 8, 12, 384, True),
+                                                  (1, 192, 5, 7, 192, False), (2, 208, 3, 33, 192, True),
+                                                  (1, 192, 1, 1, 192, True)])
+def test_conv2d_glu_3x3_winograd_matches_oracle(lib, oracle, b, ic, h, w, C, with_skip):
+    r = rng(ic + h * w)
+    x = r.uniform(-0.4, 0.4, (b, ic, h, w)).astype(np.float32)
+    skip = r.uniform(-0.4, 0.4, (b, ic, h, w)).astype(np.float32) if with_skip else np.zeros_like(x)
+    wt = r.uniform(-0.1, 0.1, (2 * C, ic, 3, 3)).astype(np.float32)
+    bias = r.uniform(-0.4, 0.4, 2 * C).astype(np.float32)
+    ref = oracle.glu(oracle.conv2d(x + skip, wt, bias, (1, 1), (1, 1)))
+    out = torch.empty(ref.shape, device="cuda")
+    dx, ds, dwt, db = dev(x), dev(skip), dev(wt), dev(bias)
+    call(lib, "dmx_op_conv2d_glu", stream(), ptr(dx), ptr(ds) if with_skip else None, b, ic, h, w, ptr(dwt),
+         ptr(db), C, 3, 3, 1, 1, None, ctypes.c_float(0.0), ptr(out))
+    assert rms_relative_error(ref, out.cpu().numpy()) < 1e-5
+
+
 def test_conv2d_glu_adds_the_frequency_embedding(lib, oracle):
     r = rng(9)
     b, ic, f, t, C = 1, 48, 16, 5, 48
