@@ -74,7 +74,7 @@ int dmx_op_conv2d_glu(void *stream, const float *x, const float *skip, int b, in
         if (kh == 3 && kw == 3 && ph == 1 && pw == 1 && !emb && winograd_applies(ic, C, h, w)) {
             // The decoder rewrite's shape: the Winograd path the runner takes for it.
             require_ptrs({x, weight, bias, out}, "conv2d_glu");
-            std::vector<float> hw((size_t)2 * C * ic * 9), u((size_t)16 * 2 * C * ic);
+            std::vector<float> hw((size_t)2 * C * ic * 9), u((size_t)winograd_weight_floats(ic, C));
             DMX_HIP(hipStreamSynchronize(s));
             DMX_HIP(hipMemcpy(hw.data(), weight, hw.size() * sizeof(float), hipMemcpyDeviceToHost));
             winograd_weights(hw.data(), 2 * C, ic, u.data());

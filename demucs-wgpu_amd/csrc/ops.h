@@ -55,14 +55,15 @@ int conv_transpose_taps(int k, int st);
 void pack_conv_transpose(const float *w, int ic, int oc, int k, int st, float *packed);
 
 // The frequency decoder's rewrite, conv2d 3x3 / padding 1 of (x + skip) from
-// ic to 2C channels, bias, GLU (host.rs:682-759), by Winograd F(2x2, 3x3)
-// (winograd.hip). U is winograd_weights() of the PyTorch (2C, ic, 3, 3) weight,
-// (16, 2C, ic); scratch holds winograd_scratch_floats() floats. skip may be
-// null. winograd_channels() says whether a layer's widths take this path (the
-// weights to prepare at load), winograd_applies() whether a call does (also
-// fp32 MFMA precision).
-bool winograd_channels(int ic, int C);
+// ic to 2C channels, bias, GLU (host.rs:682-759), by Winograd F(m x m, 3x3)
+// (winograd.hip). winograd_tile() is the m a layer's widths take (0: the
+// direct path; it decides which weights to prepare at load), winograd_applies()
+// whether a call takes it (also fp32 MFMA precision). U is winograd_weights()
+// of the PyTorch (2C, ic, 3, 3) weight, winograd_weight_floats() floats
+// ((m+2)^2, 2C, ic); scratch holds winograd_scratch_floats(). skip may be null.
+int winograd_tile(int ic, int C);
 bool winograd_applies(int ic, int C, int F, int T);
+int64_t winograd_weight_floats(int ic, int C);
 int64_t winograd_scratch_floats(int B, int ic, int C, int F, int T);
 void winograd_weights(const float *w, int oc, int ic, float *U);
 void conv3x3_glu_winograd(hipStream_t s, const float *x, const float *skip, int B, int ic, int C, int F, int T,

@@ -912,8 +912,8 @@ void load_weights(dmx_runner &r, const dmx_tensor *weights, size_t n) {
         L.conv_b = dev(r, d + ".conv_tr.bias");
         L.rw = gemm_order(d + ".rewrite.weight", 2 * L.cin, L.cin, 3, 3);
         L.rb = dev(r, d + ".rewrite.bias");
-        if (winograd_channels(L.cin, L.cin)) {
-            std::vector<float> u((size_t)16 * 2 * L.cin * L.cin);
+        if (winograd_tile(L.cin, L.cin)) {
+            std::vector<float> u((size_t)winograd_weight_floats(L.cin, L.cin));
             winograd_weights(given[d + ".rewrite.weight"]->data, 2 * L.cin, L.cin, u.data());
             L.rw_wino = upload(r, u);
         }
