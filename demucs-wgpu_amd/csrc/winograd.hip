@@ -224,7 +224,7 @@ void run(hipStream_t s, const float *x, const float *skip, int B, int ic, int C,
 #define DMX_WINO_TILE 4
 #endif
 #ifndef DMX_WINO_MIN_C
-#define DMX_WINO_MIN_C 192
+#define DMX_WINO_MIN_C 96
 #endif
 static_assert(DMX_WINO_TILE == 0 || DMX_WINO_TILE == 2 || DMX_WINO_TILE == 4, "the Winograd tile is 2 or 4");
 

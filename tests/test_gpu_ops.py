@@ -114,12 +114,14 @@ def test_conv2d_glu_matches_oracle(lib, oracle, b, ic, h, w, C, kh, kw):
     assert rms_relative_error(ref, out.cpu().numpy()) < 1e-5
 
 
-# 3x3 / padding 1 with at least 192 output channels: the decoder rewrite's
-# shape, which runs as Winograd F(2x2, 3x3) (input transform, 16 batched GEMMs,
-# output transform + GLU); odd sizes leave partial 2x2 tiles at the edges.
+# 3x3 / padding 1 with at least 96 output channels: the decoder rewrite's
+# shape, which runs as Winograd F(4x4, 3x3) (input transform, 36 batched GEMMs,
+# output transform + GLU); sizes that are not multiples of 4 leave partial
+# tiles at the edges.
 @pytest.mark.parametrize("b,ic,h,w,C,with_skip", [(2, 192, 8, 20, 192, True), (1, 384, 8, 12, 384, True),
                                                   (1, 192, 5, 7, 192, False), (2, 208, 3, 33, 192, True),
-                                                  (1, 192, 1, 1, 192, True)])
+                                                  (1, 192, 1, 1, 192, True), (2, 96, 16, 21, 96, True),
+                                                  (1, 96, 32, 336, 96, True)])
 def test_conv2d_glu_3x3_winograd_matches_oracle(lib, oracle, b, ic, h, w, C, with_skip):
     r = rng(ic + h * w)
     x = r.uniform(-0.4, 0.4, (b, ic, h, w)).astype(np.float32)
