@@ -123,6 +123,10 @@ __global__ __launch_bounds__(256) void channels_to_tokens_ln_kernel(const float 
 
 // MyGroupNorm(1, C) on token planes (crates/demucs-core/src/demucs/host.rs:1137-1196):
 // scale = inv * w[c], shift = bias[c] - mean * scale, x = x * scale + shift.
+// The grid stride is a multiple of the row's C/4 float4s, so each thread keeps
+// one channel quad: its scale and shift are computed once, and the loop is a
+// float4 load, four FMAs and a store, GN_UNROLL loads in flight.
+constexpr int GN_UNROLL = 4;
 __global__ __launch_bounds__(256) void gn_tokens_apply_kernel(float4 *__restrict__ x, int64_t per_batch4, int C4,
                                                               const double *__restrict__ stats, double count,
                                                               const float4 *__restrict__ w,
@@ -131,16 +135,34 @@ __global__ __launch_bounds__(256) void gn_tokens_apply_kernel(float4 *__restrict
     float mean, inv;
     gn_stats(stats + 2 * b, count, mean, inv);
     float4 *xb = x + b * per_batch4;
-    for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < per_batch4; i += (int64_t)gridDim.x * 256) {
-        int c4 = (int)(i % C4);
-        float4 ww = w[c4], bb = bias[c4], v = xb[i];
-        float sx = inv * ww.x, sy = inv * ww.y, sz = inv * ww.z, sw = inv * ww.w;
-        v.x = v.x * sx + (bb.x - mean * sx);
-        v.y = v.y * sy + (bb.y - mean * sy);
-        v.z = v.z * sz + (bb.z - mean * sz);
-        v.w = v.w * sw + (bb.w - mean * sw);
-        xb[i] = v;
+    const int64_t start = (int64_t)blockIdx.x * 256 + threadIdx.x, stride = (int64_t)gridDim.x * 256;
+    const int c4 = (int)(start % C4);
+    const float4 ww = w[c4], bb = bias[c4];
+    const float4 sc = make_float4(inv * ww.x, inv * ww.y, inv * ww.z, inv * ww.w);
+    const float4 sh = make_float4(bb.x - mean * sc.x, bb.y - mean * sc.y, bb.z - mean * sc.z, bb.w - mean * sc.w);
+    auto apply = [&](float4 v) {
+        return make_float4(fmaf(v.x, sc.x, sh.x), fmaf(v.y, sc.y, sh.y), fmaf(v.z, sc.z, sh.z), fmaf(v.w, sc.w, sh.w));
+    };
+    if (stride % C4 != 0) {  // the channel quad changes along the loop
+        for (int64_t i = start; i < per_batch4; i += stride) {
+            const int q = (int)(i % C4);
+            const float4 wq = w[q], bq = bias[q], v = xb[i];
+            xb[i] = make_float4(fmaf(v.x, inv * wq.x, bq.x - mean * inv * wq.x),
+                                fmaf(v.y, inv * wq.y, bq.y - mean * inv * wq.y),
+                                fmaf(v.z, inv * wq.z, bq.z - mean * inv * wq.z),
+                                fmaf(v.w, inv * wq.w, bq.w - mean * inv * wq.w));
+        }
+        return;
     }
+    int64_t i = start;
+    for (; i + (GN_UNROLL - 1) * stride < per_batch4; i += GN_UNROLL * stride) {
+        float4 v[GN_UNROLL];
+#pragma unroll
+        for (int u = 0; u < GN_UNROLL; ++u) v[u] = xb[i + u * stride];
+#pragma unroll
+        for (int u = 0; u < GN_UNROLL; ++u) xb[i + u * stride] = apply(v[u]);
+    }
+    for (; i < per_batch4; i += stride) xb[i] = apply(xb[i]);
 }
 
 // f64 moments of each (batch, group) run of `len` floats.
@@ -249,7 +271,10 @@ void group_norm_tokens_apply(hipStream_t s, float *x, int b, int L, int C, const
     require_ptrs({x, stats, w, bias}, "group_norm_tokens_apply");
     DMX_REQUIRE(C % 4 == 0, "group_norm_tokens_apply: channels must be a multiple of 4");
     int64_t per4 = (int64_t)L * C / 4;
-    dim3 grid(grid_for(per4, 2048), (unsigned)b);
+    // About 8 float4 per thread; a stride that keeps each thread on one channel
+    // quad when C/4 divides 256 (C = 512: 128 quads).
+    const int64_t blocks = std::min<int64_t>(std::max<int64_t>(1, per4 / (256 * 2 * GN_UNROLL)), 65535);
+    dim3 grid((unsigned)blocks, (unsigned)b);
     hipLaunchKernelGGL(gn_tokens_apply_kernel, grid, dim3(256), 0, s, reinterpret_cast<float4 *>(x), per4, C / 4,
                        stats, (double)L * (double)C, reinterpret_cast<const float4 *>(w),
                        reinterpret_cast<const float4 *>(bias));
