@@ -27,7 +27,14 @@
 //     when some query's tile max exceeds it by more than ATT_SLACK, so the
 //     accumulator rescale is skipped on most tiles while exp2(s - m) stays
 //     below 2^ATT_SLACK. O and the row sum carry the same factor, which the
-//     final division cancels.
+//     final division cancels. The score MFMAs accumulate onto -m rather than
+//     0, so they deliver s - m and the exponentials need no subtraction.
+//   * K/V tiles are fetched through buffer resources (scalar base and size,
+//     32-bit lane offsets): no per-tile address arithmetic on the VALU.
+//   * The file is compiled with -fno-honor-nans: no NaN reaches the kernels
+//     from finite inputs, and the row maxima then take no canonicalising
+//     v_max per score.
+#include <algorithm>
 #include <type_traits>
 #include <utility>
 
@@ -54,6 +61,12 @@ constexpr float ATT_LOG2E = 1.4426950408889634f;
 constexpr float ATT_SLACK = 8.0f;
 
 __device__ __forceinline__ float4 lds4(const float *p) { return *reinterpret_cast<const float4 *>(p); }
+
+// Raw buffer resource over `bytes` bytes from `base` (gfx9 word 3: 32-bit
+// raw data format). Loads at offsets >= bytes return zeros.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t att_rsrc(const float *base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<float *>(base), (short)0, (int)bytes, 0x00020000);
+}
 
 // One launch covers up to two attention problems (the two branches of a
 // transformer layer): blocks [0, p[0].blocks) work on p[0], the rest on p[1].
@@ -144,15 +157,28 @@ void attention_kernel(const AttGroup g) {
     floatx4 kpre[4], vpre[4];  // vector values: they stay in VGPRs
     auto slot_key = [&](int i) { return 16 * ((4 * wave + i) & 3) + (lane & 15); };
     auto slot_d4 = [&](int i) { return 4 * ((4 * wave + i) >> 2) + (lane >> 4); };
-    // Keys past n_k (ragged last tile) repeat the last key: their scores are
-    // masked to -inf, so those rows never contribute. Branch-free, so the
-    // loads stay ahead of the tile's MFMAs.
+    // Byte offsets of the slots from the tile's first key row. Each tile is
+    // read through a buffer resource (wave-uniform base and size) plus these
+    // 32-bit lane offsets, so no per-tile address arithmetic runs on the
+    // VALU. The resource ends at this (row, head)'s last key: slots past n_k
+    // (a ragged last tile) read as zeros, and the mask discards their scores.
+    uint32_t kofs[4], vofs[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        kofs[i] = (uint32_t)((slot_key(i) * ldk + 4 * slot_d4(i)) * sizeof(float));
+        vofs[i] = (uint32_t)((slot_key(i) * ldv + 4 * slot_d4(i)) * sizeof(float));
+    }
+    const uint32_t kbytes = (uint32_t)(((int64_t)(n_k - 1) * ldk + ATT_D) * sizeof(float));
+    const uint32_t vbytes = (uint32_t)(((int64_t)(n_k - 1) * ldv + ATT_D) * sizeof(float));
     auto fetch = [&](int key0) {
+        const __amdgpu_buffer_rsrc_t rk =
+            att_rsrc(kb + (int64_t)key0 * ldk, kbytes - (uint32_t)(key0 * ldk * sizeof(float)));
+        const __amdgpu_buffer_rsrc_t rv =
+            att_rsrc(vb + (int64_t)key0 * ldv, vbytes - (uint32_t)(key0 * ldv * sizeof(float)));
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            const int kk = min(key0 + slot_key(i), n_k - 1), d = 4 * slot_d4(i);
-            kpre[i] = *reinterpret_cast<const floatx4 *>(kb + (int64_t)kk * ldk + d);
-            vpre[i] = *reinterpret_cast<const floatx4 *>(vb + (int64_t)kk * ldv + d);
+            kpre[i] = __builtin_bit_cast(floatx4, __builtin_amdgcn_raw_buffer_load_b128(rk, kofs[i], 0, 0));
+            vpre[i] = __builtin_bit_cast(floatx4, __builtin_amdgcn_raw_buffer_load_b128(rv, vofs[i], 0, 0));
         }
     };
     auto stage = [&](int buf) {
@@ -170,11 +196,18 @@ void attention_kernel(const AttGroup g) {
     const floatx16 zero = {};
     floatx16 o0 = zero, o1 = zero;
     float m_run = -INFINITY, l_run = 0.0f;
+    // The score accumulators start at -mb (in every register) instead of 0,
+    // so the MFMAs deliver s - mb: mb is the running max once the first tile
+    // has set it (0 before), and the common tile needs no subtraction before
+    // its exponentials. thr is the rescale threshold on s - mb: -inf until
+    // the first tile, then ATT_SLACK.
+    floatx16 negmb = zero;
+    float mb = 0.0f, thr = -INFINITY;
 
     // One 64-key tile; MASK only for a ragged last tile.
     auto tile = [&](auto mask_tag, int buf, int key0) {
         constexpr bool MASK = decltype(mask_tag)::value;
-        // S^T for keys [key0, key0+32) (s0) and [key0+32, key0+64) (s1).
+        // S^T - mb for keys [key0, key0+32) (s0) and [key0+32, key0+64) (s1).
         floatx16 s0, s1;
 #pragma unroll
         for (int c = 0; c < 8; ++c) {
@@ -185,8 +218,8 @@ void attention_kernel(const AttGroup g) {
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
                 const int s = 4 * c + e;
-                s0 = __builtin_amdgcn_mfma_f32_32x32x2f32(av[e], qreg[s], s == 0 ? zero : s0, 0, 0, 0);
-                s1 = __builtin_amdgcn_mfma_f32_32x32x2f32(cv[e], qreg[s], s == 0 ? zero : s1, 0, 0, 0);
+                s0 = __builtin_amdgcn_mfma_f32_32x32x2f32(av[e], qreg[s], s == 0 ? negmb : s0, 0, 0, 0);
+                s1 = __builtin_amdgcn_mfma_f32_32x32x2f32(cv[e], qreg[s], s == 0 ? negmb : s1, 0, 0, 0);
             }
         }
         // Register r of lane l holds key key0 + 8*(r/4) + 4*half + r%4 (s0), +32 (s1).
@@ -202,22 +235,28 @@ void attention_kernel(const AttGroup g) {
 #pragma unroll
         for (int r = 1; r < 16; ++r) mloc = fmaxf(mloc, fmaxf(s0[r], s1[r]));
         mloc = fmaxf(mloc, __shfl_xor(mloc, 32, 64));
-        if (__any(mloc > m_run + ATT_SLACK)) {  // uniform branch; always taken on the first tile
-            const float m_new = fmaxf(m_run, mloc);
-            const float corr = __builtin_amdgcn_exp2f(m_run - m_new);
+        if (__any(mloc > thr)) {  // uniform branch; always taken on the first tile
+            const float m_new = fmaxf(m_run, mloc + mb);
+            const float corr = __builtin_amdgcn_exp2f(m_run - m_new);  // 0 on the first tile: O, l are 0
+            const float shift = m_new - mb;
             l_run *= corr;
             m_run = m_new;
+            mb = m_new;
+            thr = ATT_SLACK;
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
                 o0[r] *= corr;
                 o1[r] *= corr;
+                s0[r] -= shift;
+                s1[r] -= shift;
+                negmb[r] = -m_new;
             }
         }
         float lsum = 0.0f;
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
-            s0[r] = __builtin_amdgcn_exp2f(s0[r] - m_run);
-            s1[r] = __builtin_amdgcn_exp2f(s1[r] - m_run);
+            s0[r] = __builtin_amdgcn_exp2f(s0[r]);
+            s1[r] = __builtin_amdgcn_exp2f(s1[r]);
             lsum += s0[r] + s1[r];
         }
         lsum += __shfl_xor(lsum, 32, 64);
@@ -247,10 +286,13 @@ void attention_kernel(const AttGroup g) {
 
     const int tiles = (n_k + ATT_KT - 1) / ATT_KT;
     const bool ragged = (n_k % ATT_KT) != 0;
+    // The loop runs the full tiles only; a ragged last tile (the one masked
+    // variant) follows it, so the loop body has a single tile variant.
+    const int full = tiles - (ragged ? 1 : 0);
     fetch(0);
     stage(0);
     __syncthreads();
-    for (int t = 0; t < tiles; ++t) {
+    for (int t = 0; t < full; ++t) {
         const int buf = t & 1;
         const bool more = t + 1 < tiles;
         // The next tile's loads go out before this tile's MFMAs (on the last
@@ -258,10 +300,7 @@ void attention_kernel(const AttGroup g) {
         // of the MFMAs by the scheduling barrier.
         fetch(min(t + 1, tiles - 1) * ATT_KT);
         __builtin_amdgcn_sched_barrier(0);
-        if (!more && ragged)
-            tile(std::true_type{}, buf, t * ATT_KT);
-        else
-            tile(std::false_type{}, buf, t * ATT_KT);
+        tile(std::false_type{}, buf, t * ATT_KT);
         if (more) {
             // The other buffer was last read in tile t-1, which every wave
             // finished before the previous barrier.
@@ -269,6 +308,7 @@ void attention_kernel(const AttGroup g) {
             __syncthreads();
         }
     }
+    if (ragged) tile(std::true_type{}, full & 1, full * ATT_KT);
 
     if (!q_ok) return;
     const float inv = l_run > 0.0f ? 1.0f / l_run : 1.0f;
@@ -474,6 +514,12 @@ void attention_grouped(hipStream_t s, const AttentionArgs *probs, int count, flo
         require_ptrs({a.q, a.k, a.v, a.out}, "attention");
         DMX_REQUIRE(a.d_head == ATT_D, "attention: only d_head = 64 is implemented");
         DMX_REQUIRE(a.n_q > 0 && a.n_k > 0 && a.batch > 0 && a.heads > 0, "attention: empty problem");
+        // K/V tiles are read through buffer resources that end at a (row,
+        // head)'s last key: rows must not overlap, and the extent must fit
+        // the resource's 31-bit size.
+        DMX_REQUIRE(a.ldk >= ATT_D && a.ldv >= ATT_D, "attention: K/V rows shorter than d_head");
+        DMX_REQUIRE(((int64_t)(a.n_k - 1) * std::max(a.ldk, a.ldv) + ATT_D) * (int64_t)sizeof(float) < (1ll << 31),
+                    "attention: K/V extent of one (row, head) exceeds 2 GiB");
         DMX_REQUIRE(a.ldq % 4 == 0 && a.ldk % 4 == 0 && a.ldv % 4 == 0 && a.ldo % 4 == 0 && a.q_batch_stride % 4 == 0 &&
                         a.kv_batch_stride % 4 == 0 && a.out_batch_stride % 4 == 0,
                     "attention: row strides must be multiples of 4 floats");
