@@ -289,6 +289,12 @@ void attention_kernel(const AttGroup g) {
     // The loop runs the full tiles only; a ragged last tile (the one masked
     // variant) follows it, so the loop body has a single tile variant.
     const int full = tiles - (ragged ? 1 : 0);
+    // A wave whose 32 queries all lie past n_q (the back half of a last query
+    // block when n_q is an odd multiple of 64) stages its share of every tile
+    // and takes part in the barriers, but skips the multiplies: its SIMD's
+    // matrix core is left to the other workgroup's wave.
+    const bool wave_active =
+        qblock * (ATT_QW * ATT_WAVES) + __builtin_amdgcn_readfirstlane(wave) * ATT_QW < n_q;
     fetch(0);
     stage(0);
     __syncthreads();
@@ -300,7 +306,7 @@ void attention_kernel(const AttGroup g) {
         // of the MFMAs by the scheduling barrier.
         fetch(min(t + 1, tiles - 1) * ATT_KT);
         __builtin_amdgcn_sched_barrier(0);
-        tile(std::false_type{}, buf, t * ATT_KT);
+        if (wave_active) tile(std::false_type{}, buf, t * ATT_KT);
         if (more) {
             // The other buffer was last read in tile t-1, which every wave
             // finished before the previous barrier.
@@ -308,7 +314,7 @@ void attention_kernel(const AttGroup g) {
             __syncthreads();
         }
     }
-    if (ragged) tile(std::true_type{}, full & 1, full * ATT_KT);
+    if (ragged && wave_active) tile(std::true_type{}, full & 1, full * ATT_KT);
 
     if (!q_ok) return;
     const float inv = l_run > 0.0f ? 1.0f / l_run : 1.0f;
