@@ -378,27 +378,37 @@ __global__ __launch_bounds__(256) void attention_bf16_kernel(const AttGroup g) {
         }
     }
 
-    float4 kpre[4], vpre[4];
+    floatx4 kpre[4], vpre[4];
     auto slot_key = [&](int i) { return 16 * ((4 * wave + i) & 3) + (lane & 15); };
     auto slot_d4 = [&](int i) { return 4 * ((4 * wave + i) >> 2) + (lane >> 4); };
-    // Keys past n_k (ragged last tile) repeat the last key: their scores are
-    // masked to -inf, so those rows never contribute. Branch-free, so the
-    // loads stay ahead of the tile's MFMAs.
+    // Tiles are read through buffer resources, as in the fp32 kernel: slots
+    // past n_k read as zeros and the mask discards their scores.
+    uint32_t kofs[4], vofs[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        kofs[i] = (uint32_t)((slot_key(i) * ldk + 4 * slot_d4(i)) * sizeof(float));
+        vofs[i] = (uint32_t)((slot_key(i) * ldv + 4 * slot_d4(i)) * sizeof(float));
+    }
+    const uint32_t kbytes = (uint32_t)(((int64_t)(n_k - 1) * ldk + ATT_D) * sizeof(float));
+    const uint32_t vbytes = (uint32_t)(((int64_t)(n_k - 1) * ldv + ATT_D) * sizeof(float));
     auto fetch = [&](int key0) {
+        const __amdgpu_buffer_rsrc_t rk =
+            att_rsrc(kb + (int64_t)key0 * ldk, kbytes - (uint32_t)(key0 * ldk * sizeof(float)));
+        const __amdgpu_buffer_rsrc_t rv =
+            att_rsrc(vb + (int64_t)key0 * ldv, vbytes - (uint32_t)(key0 * ldv * sizeof(float)));
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            const int kk = min(key0 + slot_key(i), n_k - 1), d = 4 * slot_d4(i);
-            kpre[i] = *reinterpret_cast<const float4 *>(kb + (int64_t)kk * ldk + d);
-            vpre[i] = *reinterpret_cast<const float4 *>(vb + (int64_t)kk * ldv + d);
+            kpre[i] = __builtin_bit_cast(floatx4, __builtin_amdgcn_raw_buffer_load_b128(rk, kofs[i], 0, 0));
+            vpre[i] = __builtin_bit_cast(floatx4, __builtin_amdgcn_raw_buffer_load_b128(rv, vofs[i], 0, 0));
         }
     };
     auto stage = [&](int buf) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const int key = slot_key(i), d = 4 * slot_d4(i);
-            const bf16x4 kv = __builtin_convertvector((floatx4){kpre[i].x, kpre[i].y, kpre[i].z, kpre[i].w}, bf16x4);
+            const bf16x4 kv = __builtin_convertvector(kpre[i], bf16x4);
             *reinterpret_cast<bf16x4 *>(&Ks[buf][key][d]) = kv;
-            const bf16x4 vv = __builtin_convertvector((floatx4){vpre[i].x, vpre[i].y, vpre[i].z, vpre[i].w}, bf16x4);
+            const bf16x4 vv = __builtin_convertvector(vpre[i], bf16x4);
             Vt[buf][d + 0][key] = vv[0];
             Vt[buf][d + 1][key] = vv[1];
             Vt[buf][d + 2][key] = vv[2];
@@ -415,10 +425,13 @@ __global__ __launch_bounds__(256) void attention_bf16_kernel(const AttGroup g) {
     const floatx16 zero = {};
     floatx16 o0 = zero, o1 = zero;
     float m_run = -INFINITY, l_run = 0.0f;
+    // Scores accumulate onto -mb, as in the fp32 kernel.
+    floatx16 negmb = zero;
+    float mb = 0.0f, thr = -INFINITY;
 
     auto tile = [&](auto mask_tag, int buf, int key0) {
         constexpr bool MASK = decltype(mask_tag)::value;
-        floatx16 s0 = zero, s1 = zero;
+        floatx16 s0 = negmb, s1 = negmb;
 #pragma unroll
         for (int t = 0; t < 4; ++t) {
             const bf16x8 ka = *reinterpret_cast<const bf16x8 *>(&Ks[buf][j][16 * t + 8 * half]);
@@ -438,22 +451,28 @@ __global__ __launch_bounds__(256) void attention_bf16_kernel(const AttGroup g) {
 #pragma unroll
         for (int r = 1; r < 16; ++r) mloc = fmaxf(mloc, fmaxf(s0[r], s1[r]));
         mloc = fmaxf(mloc, __shfl_xor(mloc, 32, 64));
-        if (__any(mloc > m_run + ATT_SLACK)) {
-            const float m_new = fmaxf(m_run, mloc);
+        if (__any(mloc > thr)) {
+            const float m_new = fmaxf(m_run, mloc + mb);
             const float corr = __builtin_amdgcn_exp2f(m_run - m_new);
+            const float shift = m_new - mb;
             l_run *= corr;
             m_run = m_new;
+            mb = m_new;
+            thr = ATT_SLACK;
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
                 o0[r] *= corr;
                 o1[r] *= corr;
+                s0[r] -= shift;
+                s1[r] -= shift;
+                negmb[r] = -m_new;
             }
         }
         float lsum = 0.0f;
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
-            s0[r] = __builtin_amdgcn_exp2f(s0[r] - m_run);
-            s1[r] = __builtin_amdgcn_exp2f(s1[r] - m_run);
+            s0[r] = __builtin_amdgcn_exp2f(s0[r]);
+            s1[r] = __builtin_amdgcn_exp2f(s1[r]);
             lsum += s0[r] + s1[r];
         }
         lsum += __shfl_xor(lsum, 32, 64);
@@ -473,23 +492,24 @@ __global__ __launch_bounds__(256) void attention_bf16_kernel(const AttGroup g) {
 
     const int tiles = (n_k + ATT_KT - 1) / ATT_KT;
     const bool ragged = (n_k % ATT_KT) != 0;
+    const int full = tiles - (ragged ? 1 : 0);
+    const bool wave_active =
+        qblock * (ATT_QW * ATT_WAVES) + __builtin_amdgcn_readfirstlane(wave) * ATT_QW < n_q;
     fetch(0);
     stage(0);
     __syncthreads();
-    for (int t = 0; t < tiles; ++t) {
+    for (int t = 0; t < full; ++t) {
         const int buf = t & 1;
         const bool more = t + 1 < tiles;
         fetch(min(t + 1, tiles - 1) * ATT_KT);
         __builtin_amdgcn_sched_barrier(0);
-        if (!more && ragged)
-            tile(std::true_type{}, buf, t * ATT_KT);
-        else
-            tile(std::false_type{}, buf, t * ATT_KT);
+        if (wave_active) tile(std::false_type{}, buf, t * ATT_KT);
         if (more) {
             stage(buf ^ 1);
             __syncthreads();
         }
     }
+    if (ragged && wave_active) tile(std::true_type{}, full & 1, full * ATT_KT);
 
     if (!q_ok) return;
     const float inv = l_run > 0.0f ? 1.0f / l_run : 1.0f;
