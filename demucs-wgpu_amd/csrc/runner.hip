@@ -427,10 +427,14 @@ void attention_outputs(dmx_runner &r, hipStream_t s, const TLayerW &L, const flo
 
 // The layers of the cross-transformer (host.rs:895-941) on the token planes
 // spec (B, Lf, D) and time (B, Lt, D), which are replaced by the outputs.
-// Per layer: the two branches' projections run concurrently (waveform on the
-// side stream), both attentions share one launch on s, then the two output
-// halves run concurrently again. Cross layers read the other branch's plane
-// of layer i - 1.
+#ifndef DMX_ATT_SPLIT
+#define DMX_ATT_SPLIT 1
+#endif
+
+// Per layer the two branches run concurrently, the waveform branch on the
+// side stream; the streams join at layer boundaries, since cross layers read
+// the other branch's plane of layer i - 1. (DMX_ATT_SPLIT=0: both attentions
+// share one launch on s between a join and a second fork.)
 void transformer_layers(dmx_runner &r, hipStream_t s, DBuf &spec, int64_t Lf, DBuf &time, int64_t Lt, int B) {
     const int D = r.tch, heads = r.cfg.t_heads;
     const float scale = 1.0f / std::sqrt((float)(D / heads));
@@ -446,6 +450,24 @@ void transformer_layers(dmx_runner &r, hipStream_t s, DBuf &spec, int64_t Lf, DB
         DBuf as = fbuf(s, B * Lf * D), at = fbuf(s, (int64_t)B * Lt * D);
         Branches br(r, s);
         br.fork();
+#if DMX_ATT_SPLIT
+        // Within a layer the branches do not depend on each other (a cross
+        // layer reads the other branch's plane of layer i - 1, which both
+        // streams have at the fork): each branch runs projections, its
+        // attention and its output half on its own stream, and the shorter
+        // time-branch chain fills the tail of the spectral attention.
+        {
+            const AttentionArgs pta =
+                attention_inputs(r, br.t, Lt_, time.f(), cross ? spec.f() : nullptr, sht, pt.f(), at.f());
+            attention_grouped(br.t, &pta, 1, scale);
+            attention_outputs(r, br.t, Lt_, time.f(), sht, at.f(), nt, nt_.f());
+            const AttentionArgs psa =
+                attention_inputs(r, s, Ls, spec.f(), cross ? time.f() : nullptr, shs, ps.f(), as.f());
+            attention_grouped(s, &psa, 1, scale);
+            attention_outputs(r, s, Ls, spec.f(), shs, as.f(), n, ns.f());
+        }
+        br.join();
+#else
         AttentionArgs prob[2];
         prob[1] = attention_inputs(r, br.t, Lt_, time.f(), cross ? spec.f() : nullptr, sht, pt.f(), at.f());
         prob[0] = attention_inputs(r, s, Ls, spec.f(), cross ? time.f() : nullptr, shs, ps.f(), as.f());
@@ -456,6 +478,7 @@ void transformer_layers(dmx_runner &r, hipStream_t s, DBuf &spec, int64_t Lf, DB
         attention_outputs(r, br2.t, Lt_, time.f(), sht, at.f(), nt, nt_.f());
         attention_outputs(r, s, Ls, spec.f(), shs, as.f(), n, ns.f());
         br2.join();
+#endif
         spec = std::move(ns);
         time = std::move(nt_);
     }
