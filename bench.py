@@ -8,8 +8,8 @@ stems written to HBM (device entry point dmx_separate_device).
 value = x-realtime = audio seconds / wall seconds over the timed steps.
 
 Also reported: the cross-attention kernel's TFLOP/s at the model's shape
-(Q 2688 vs K/V 1344 and Q 1344 vs K/V 2688 in one launch, as the runner
-issues a cross layer's two branches; 8 heads x 64, batch 8) and its roofline
+(Q 2688 vs K/V 1344 and Q 1344 vs K/V 2688, a cross layer's two directions,
+in one launch; 8 heads x 64, batch 8) and its roofline
 fraction against the fp32 MFMA peak, measured with HIP events on the launch
 stream; and the
 restated reference CPU backend (oracle/) timed on this host on one 7.8 s
@@ -45,10 +45,11 @@ def load_package():
 
 
 def attention_roofline(pkg, torch, batch: int, iters: int):
-    """Average duration of the fused cross-attention launch as the runner
-    issues it in the cross layers: both directions of the model's cross shape
-    in one launch (Lq = 2688 spectral tokens vs Lk = 1344 waveform tokens, and
-    Lq = 1344 vs Lk = 2688), timed with events on the stream it is launched on.
+    """Average duration of the fused cross-attention kernel on a cross
+    layer's work: both directions of the model's cross shape in one launch
+    (Lq = 2688 spectral tokens vs Lk = 1344 waveform tokens, and Lq = 1344 vs
+    Lk = 2688; the runner issues them as two concurrent launches on the branch
+    streams), timed with events on the stream it is launched on.
     Returns (ms per launch, algorithmic flops per launch)."""
     from demucs_wgpu_amd import _native
     lib = _native.load()
@@ -320,7 +321,7 @@ def main():
                 "frac": round(attn_tflops / FP32_MFMA_PEAK_TFLOPS, 4), "traffic": measured_traffic(),
                 "kernel": "attention_kernel (fused cross-attention, fp32 MFMA)",
                 "per_launch": f"sum of 4*B*Lq*Lk*512 flops over (Lq, Lk) = (2688, 1344) and (1344, 2688), "
-                              f"B={args.batch_chunks}, both in one launch as the runner issues them; "
+                              f"B={args.batch_chunks}, both directions in one launch (dmx_op_attention_pair); "
                               f"avg {attn_ms:.3f} ms per launch"}
     line = {
         "metric": "htdemucs x-realtime (audio s / wall s) on 1 MI355X; cross-attn TFLOP/s",
