@@ -291,6 +291,51 @@ struct EpConvT : EpBase {
         if (a < 0 || a >= a_out) return;
         out[(((int64_t)z * oc + o) * a_out + a) * P + t] = act_apply(act, v + bias[o]);
     }
+    // Whole fragments (stride 4, the model's): register r of fragment (i, j)
+    // is row mb + 32 i + 8 (r / 4) + 4 khalf + r % 4 with mb a multiple of 4,
+    // i.e. channel mb / 4 + 8 i + 2 (r / 4) + khalf at phase r % 4, so the
+    // column's (qi, t) and the four phases' output offsets are worked out
+    // once per column instead of once per element.
+    static constexpr bool frags = true;
+    template <int TM, int TN>
+    __device__ void store_frags(int z, int mb, int nb, int col, int khalf, const floatx16 (&v)[TM][TN]) {
+        if (st != 4) {
+#pragma unroll
+            for (int j = 0; j < TN; ++j)
+#pragma unroll
+                for (int i = 0; i < TM; ++i)
+#pragma unroll
+                    for (int r = 0; r < 16; ++r)
+                        store(z, mb + 32 * i + 8 * (r / 4) + 4 * khalf + r % 4, nb + 32 * j + col, v[i][j][r]);
+            return;
+        }
+        const int64_t plane = (int64_t)a_out * P;
+        float *zo = out + (int64_t)z * oc * plane;
+#pragma unroll
+        for (int j = 0; j < TN; ++j) {
+            const int n = nb + 32 * j + col;
+            const int qi = n / P, t = n - qi * P;
+            const int a0 = 4 * (q0 + qi) - crop;
+            int64_t off[4];
+            bool ok[4];
+#pragma unroll
+            for (int p = 0; p < 4; ++p) {
+                ok[p] = a0 + p >= 0 && a0 + p < a_out;
+                off[p] = (int64_t)(a0 + p) * P + t;
+            }
+#pragma unroll
+            for (int i = 0; i < TM; ++i)
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    const int o = mb / 4 + 8 * i + 2 * q + khalf;
+                    const float bo = bias[o];
+                    float *ro = zo + (int64_t)o * plane;
+#pragma unroll
+                    for (int p = 0; p < 4; ++p)
+                        if (ok[p]) ro[off[p]] = act_apply(act, v[i][j][4 * q + p] + bo);
+                }
+        }
+    }
 };
 
 // DConv conv1: y = conv + bias stored as (rows, H, T); GN statistics per row.

@@ -95,6 +95,14 @@ template <class L, class = void>
 struct has_load_raw : std::false_type {};
 template <class L>
 struct has_load_raw<L, std::void_t<typename L::Raw>> : std::true_type {};
+// An epilogue may take a wave's whole fragments of a tile that lies wholly in
+// range (store_frags, announced by a `frags` member): it can then hoist the
+// per-column and per-row index arithmetic out of the element loop.
+template <class E, class = void>
+struct has_store_frags : std::false_type {};
+template <class E>
+struct has_store_frags<E, std::void_t<decltype(E::frags)>> : std::true_type {};
+
 template <class L, bool = has_load_raw<L>::value>
 struct raw_of {
     using type = float4;
@@ -329,6 +337,13 @@ __global__ __launch_bounds__(GEMM_THREADS) void gemm_kernel(int M, int N, int K,
     }
 
     // ---- epilogue ----
+    if constexpr (!GLU && has_store_frags<EP>::value) {
+        if (m_block + BM <= M && n0 + BN <= N) {
+            ep.store_frags(z, m_block + wm * WTM, n0 + wn * WTN, row_in, khalf, acc);
+            ep.finalize(z);
+            return;
+        }
+    }
 #pragma unroll
     for (int j = 0; j < TN; ++j) {
         const int n = n0 + wn * WTN + j * 32 + row_in;
