@@ -366,21 +366,36 @@ struct EpConv2Stats {
 
 // DConv conv2, second pass: GN -> GLU -> LayerScale -> residual add into x,
 // whose rows (b, f) live in a (B, C, F, T) tensor.
+// Per-channel affines of the conv2 epilogue, one table per workgroup.
+constexpr int C2A_MAXC = 768;
+__shared__ float4 c2a_affine[C2A_MAXC];
+
 struct EpConv2Apply {
     float *x;
     const float *bias, *nw, *nb, *gamma;
     const double *stats;
     int C, F, T;
-    float mean, inv;
-    __device__ void init(int z) { gn_stats(stats + 2 * z, 2.0 * C * (double)T, mean, inv); }
-    __device__ void glu(int z, int c, int n, float v, float g) {
-        float vs = inv * nw[c], vsh = nb[c] - mean * vs;
-        float gs = inv * nw[C + c], gsh = nb[C + c] - mean * gs;
-        float value = (v + bias[c]) * vs + vsh;
-        float gate = (g + bias[C + c]) * gs + gsh;
-        int b = z / F, f = z - b * F;
-        float *dst = x + (((int64_t)b * C + c) * F + f) * T + n;
-        *dst += gamma[c] * (value * sigmoid(gate));
+    float *xz;  // this row's (b, f) plane origin in x
+    // GN2 of the row and the channel's bias, GN affine and LayerScale fold
+    // into value' = v * a.x + a.y (LayerScale included) and gate' = g * a.z + a.w,
+    // one float4 per channel in LDS: the element loop then reads one LDS
+    // quad per element instead of seven scattered parameters. (The kernel's
+    // first barrier comes before its epilogue.)
+    __device__ void init(int z) {
+        float mean, inv;
+        gn_stats(stats + 2 * z, 2.0 * C * (double)T, mean, inv);
+        for (int c = threadIdx.x; c < C; c += blockDim.x) {
+            const float vs = inv * nw[c], gs = inv * nw[C + c];
+            const float vsh = (bias[c] - mean) * vs + nb[c], gsh = (bias[C + c] - mean) * gs + nb[C + c];
+            c2a_affine[c] = make_float4(gamma[c] * vs, gamma[c] * vsh, gs, gsh);
+        }
+        const int b = z / F, f = z - b * F;
+        xz = x + ((int64_t)b * C * F + f) * T;
+    }
+    __device__ void glu(int, int c, int n, float v, float g) {
+        const float4 a = c2a_affine[c];
+        float *dst = xz + (int64_t)c * F * T + n;
+        *dst += fmaf(v, a.x, a.y) * sigmoid(fmaf(g, a.z, a.w));
     }
     __device__ void finalize(int) {}
 };
@@ -775,6 +790,7 @@ void dconv_layer(hipStream_t s, float *x, int B, int C, int F, int T, int dil, c
     require_ptrs({x, w1, w1_gemm, b1, n1w, n1b, w2, b2, n2w, n2b, gamma, hbuf, stats}, "dconv_layer");
     const int rows = B * F;
     DMX_REQUIRE(rows <= 65535, "dconv_layer: too many rows for one launch");
+    DMX_REQUIRE(C <= C2A_MAXC, "dconv_layer: more channels than the conv2 epilogue's table holds");
     if (dconv_narrow_applies(C, H)) {
         dconv_layer_narrow(s, x, B, C, F, T, dil, w1, w1_t, b1, H, n1w, n1b, w2, b2, n2w, n2b, gamma, hbuf);
         return;
