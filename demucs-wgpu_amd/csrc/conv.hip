@@ -269,11 +269,60 @@ struct EpGlu : EpBase {
     float emb_scale;
     int64_t batch_stride;
     int N, C, T;
+    bool vec;  // bias 16-byte aligned and C a multiple of 4: glu_frags may read float4 biases
     __device__ void glu(int z, int c, int n, float v, float g) {
         float a = v + bias[c], gate = g + bias[C + c];
         float y = a * sigmoid(gate);
         if (emb) y += emb_scale * emb[(n / T) * C + c];
         out[z * batch_stride + (int64_t)c * N + n] = y;
+    }
+    // Whole fragments of a wave holding GCH value channels from cb and their
+    // gates: the value rows of 8-row block b = 32 i + 8 q are channels
+    // cb + b + 4 khalf + p (p = r % 4), their gates sit GCH rows further on
+    // (fragment (b + GCH) / 32, register 4 ((b + GCH) % 32 / 8) + p). Each
+    // block's four biases are one float4 (cb and C are multiples of 4; the
+    // launcher checks C), and the embedding row is found once per column.
+    static constexpr bool frags = true;
+    template <int GCH, int TM, int TN>
+    __device__ void glu_frags(int z, int cb, int nb, int col, int khalf, const floatx16 (&v)[TM][TN]) {
+        if (!vec) {
+#pragma unroll
+            for (int j = 0; j < TN; ++j)
+#pragma unroll
+                for (int i = 0; i < TM; ++i)
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) {
+                        const int b = 32 * i + 8 * (r / 4);
+                        if (b >= GCH) continue;
+                        const int gi = (b + GCH) / 32, gr = (((b + GCH) % 32) / 8) * 4 + r % 4;
+                        glu(z, cb + b + 4 * khalf + r % 4, nb + 32 * j + col, v[i][j][r], v[gi][j][gr]);
+                    }
+            return;
+        }
+        float *zo = out + z * batch_stride;
+#pragma unroll
+        for (int j = 0; j < TN; ++j) {
+            const int n = nb + 32 * j + col;
+            const float *er = emb ? emb + (n / T) * C : nullptr;
+#pragma unroll
+            for (int i = 0; i < TM; ++i)
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    const int b = 32 * i + 8 * q;
+                    if (b >= GCH) continue;
+                    const int gi = (b + GCH) / 32, gq = ((b + GCH) % 32) / 8;
+                    const int c0 = cb + b + 4 * khalf;
+                    const float4 bv = *reinterpret_cast<const float4 *>(bias + c0);
+                    const float4 bg = *reinterpret_cast<const float4 *>(bias + C + c0);
+                    const float bva[4] = {bv.x, bv.y, bv.z, bv.w}, bga[4] = {bg.x, bg.y, bg.z, bg.w};
+#pragma unroll
+                    for (int p = 0; p < 4; ++p) {
+                        float y = (v[i][j][4 * q + p] + bva[p]) * sigmoid(v[gi][j][4 * gq + p] + bga[p]);
+                        if (er) y += emb_scale * er[c0 + p];
+                        zo[(int64_t)(c0 + p) * N + n] = y;
+                    }
+                }
+        }
     }
 };
 
@@ -728,6 +777,7 @@ void conv2d_glu(hipStream_t s, const float *x, const float *skip, int b, int ic,
     ep.N = N;
     ep.C = C;
     ep.T = ow;
+    ep.vec = aligned16(bias) && C % 4 == 0;
     conv_dispatch<true>(s, C, N, K, b, kmajor(weight, K, 0), x, skip, (int64_t)ic * h * w, 0, 1, h, h, w, kh, kw, 1, 1,
                         ph, pw, 1, 1, ow, ep);
 }

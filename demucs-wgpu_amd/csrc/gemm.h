@@ -337,11 +337,19 @@ __global__ __launch_bounds__(GEMM_THREADS) void gemm_kernel(int M, int N, int K,
     }
 
     // ---- epilogue ----
-    if constexpr (!GLU && has_store_frags<EP>::value) {
-        if (m_block + BM <= M && n0 + BN <= N) {
-            ep.store_frags(z, m_block + wm * WTM, n0 + wn * WTN, row_in, khalf, acc);
-            ep.finalize(z);
-            return;
+    if constexpr (has_store_frags<EP>::value) {
+        if constexpr (GLU) {
+            if (m_block + BM / 2 <= M && n0 + BN <= N) {
+                ep.template glu_frags<GCH>(z, m_block + wm * GCH, n0 + wn * WTN, row_in, khalf, acc);
+                ep.finalize(z);
+                return;
+            }
+        } else {
+            if (m_block + BM <= M && n0 + BN <= N) {
+                ep.store_frags(z, m_block + wm * WTM, n0 + wn * WTN, row_in, khalf, acc);
+                ep.finalize(z);
+                return;
+            }
         }
     }
 #pragma unroll
