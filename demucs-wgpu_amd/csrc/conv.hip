@@ -255,9 +255,40 @@ struct EpChannels : EpBase {
     const float *bias;
     int64_t batch_stride;
     int N, act;
+    bool vec;  // bias null or 16-byte aligned: store_frags may read float4 biases
     __device__ void store(int z, int m, int n, float v) {
         float b = bias ? bias[m] : 0.0f;
         out[z * batch_stride + (int64_t)m * N + n] = act_apply(act, v + b);
+    }
+    // Whole fragments: register r of fragment (i, j) is row mb + 32 i + 8 (r / 4)
+    // + 4 khalf + r % 4, so each run of four registers takes one float4 of
+    // biases (mb is a multiple of 4).
+    static constexpr bool frags = true;
+    template <int TM, int TN>
+    __device__ void store_frags(int z, int mb, int nb, int col, int khalf, const floatx16 (&v)[TM][TN]) {
+        float *zo = out + z * batch_stride;
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const int m0 = mb + 32 * i + 8 * q + 4 * khalf;
+                float ba[4] = {0.f, 0.f, 0.f, 0.f};
+                if (bias) {
+                    if (vec) {
+                        const float4 b4 = *reinterpret_cast<const float4 *>(bias + m0);
+                        ba[0] = b4.x, ba[1] = b4.y, ba[2] = b4.z, ba[3] = b4.w;
+                    } else {
+#pragma unroll
+                        for (int p = 0; p < 4; ++p) ba[p] = bias[m0 + p];
+                    }
+                }
+#pragma unroll
+                for (int j = 0; j < TN; ++j) {
+                    float *o = zo + (int64_t)m0 * N + nb + 32 * j + col;
+#pragma unroll
+                    for (int p = 0; p < 4; ++p) o[(int64_t)p * N] = act_apply(act, v[i][j][4 * q + p] + ba[p]);
+                }
+            }
     }
 };
 
@@ -741,6 +772,7 @@ void conv2d(hipStream_t s, const float *x, const float *skip, int b, int ic, int
     ep.batch_stride = (int64_t)oc * N;
     ep.N = N;
     ep.act = act;
+    ep.vec = !ep.bias || aligned16(ep.bias);
     conv_dispatch<false>(s, oc, N, K, b, kmajor(weight, K, 0), x, skip, (int64_t)ic * h * w, 0, 1, h, h, w, kh, kw, sh,
                          sw, ph, pw, dh, dw, ow, ep);
 }
@@ -756,6 +788,7 @@ void conv1d_right_padded(hipStream_t s, const float *x, int b, int ic, int len, 
     ep.batch_stride = (int64_t)oc * ow;
     ep.N = ow;
     ep.act = act;
+    ep.vec = !ep.bias || aligned16(ep.bias);
     // Bounds use the unpadded length: the right pad is zeros either way.
     conv_dispatch<false>(s, oc, ow, K, b, kmajor(weight, K, 0), x, nullptr, (int64_t)ic * len, 0, 1, 1, 1, len, 1, k, 1,
                          stride, 0, pad, 1, 1, ow, ep);
@@ -890,6 +923,7 @@ void pointwise(hipStream_t s, const float *w, const float *bias, const float *x,
     ep.batch_stride = (int64_t)M * N;
     ep.N = N;
     ep.act = act;
+    ep.vec = !ep.bias || aligned16(ep.bias);
     gemm_auto<false>(s, M, N, K, batches, kmajor(w, K, 0), MNMajor{x, N, (int64_t)K * N}, ep);
 }
 
@@ -931,6 +965,7 @@ void tokens_to_channels(hipStream_t s, const float *tok, int b, int F, int T, in
     ep.batch_stride = (int64_t)M * F * T;
     ep.N = F * T;
     ep.act = ACT_NONE;
+    ep.vec = !ep.bias || aligned16(ep.bias);
     // A rearrange (w is the identity in the transformer-only path): kept in
     // fp32 whatever the precision scope, so it stays exact.
     gemm_pick<false, false>(s, M, F * T, D, b, kmajor(w, D, 0), TokenGather{tok, F, T, D}, ep);
