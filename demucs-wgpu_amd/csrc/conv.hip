@@ -438,9 +438,43 @@ struct EpConv1 {
 struct EpConv2Stats {
     const float *bias;
     double *stats;
+    bool vec;  // bias 16-byte aligned
     MomentAcc acc;
     __device__ void init(int) {}
     __device__ void store(int, int m, int, float v) { acc.add(v + bias[m]); }
+    // Whole fragments: each run of four registers (four consecutive rows)
+    // takes one float4 of biases and enters the f64 moments as one fp32
+    // partial sum of four values and one of their squares.
+    static constexpr bool frags = true;
+    template <int TM, int TN>
+    __device__ void store_frags(int, int mb, int, int, int khalf, const floatx16 (&v)[TM][TN]) {
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const int m0 = mb + 32 * i + 8 * q + 4 * khalf;
+                float ba[4];
+                if (vec) {
+                    const float4 b4 = *reinterpret_cast<const float4 *>(bias + m0);
+                    ba[0] = b4.x, ba[1] = b4.y, ba[2] = b4.z, ba[3] = b4.w;
+                } else {
+#pragma unroll
+                    for (int p = 0; p < 4; ++p) ba[p] = bias[m0 + p];
+                }
+#pragma unroll
+                for (int j = 0; j < TN; ++j) {
+                    float s4 = 0.0f, q4 = 0.0f;
+#pragma unroll
+                    for (int p = 0; p < 4; ++p) {
+                        const float x = v[i][j][4 * q + p] + ba[p];
+                        s4 += x;
+                        q4 = fmaf(x, x, q4);
+                    }
+                    acc.s += (double)s4;
+                    acc.q += (double)q4;
+                }
+            }
+    }
     __device__ void finalize(int z) { acc.flush(stats + 2 * z); }
 };
 
@@ -893,6 +927,7 @@ void dconv_layer(hipStream_t s, float *x, int B, int C, int F, int T, int dil, c
     EpConv2Stats e2;
     e2.bias = b2;
     e2.stats = st2;
+    e2.vec = aligned16(b2);
     EpConv2Apply e3;
     e3.x = x;
     e3.bias = b2;
