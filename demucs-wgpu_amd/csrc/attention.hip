@@ -62,6 +62,29 @@ constexpr float ATT_SLACK = 8.0f;
 
 __device__ __forceinline__ float4 lds4(const float *p) { return *reinterpret_cast<const float4 *>(p); }
 
+// A wave raises its issue priority (s_setprio 1) for its two runs of MFMAs
+// per tile and drops it for the softmax: when both waves on a SIMD are ready,
+// the one feeding the matrix core issues first, and the other's softmax fills
+// the matrix core's busy cycles (0.997-1.003 against 1.016 ms per paired
+// cross launch). DMX_ATT_SETPRIO=0 builds without it.
+#ifndef DMX_ATT_SETPRIO
+#define DMX_ATT_SETPRIO 1
+#endif
+template <int P>
+__device__ __forceinline__ void att_prio_imm() {
+    __builtin_amdgcn_s_setprio(P);
+}
+__device__ __forceinline__ void att_prio(int p) {
+#if DMX_ATT_SETPRIO
+    if (p)
+        att_prio_imm<1>();
+    else
+        att_prio_imm<0>();
+#else
+    (void)p;
+#endif
+}
+
 // Raw buffer resource over `bytes` bytes from `base` (gfx9 word 3: 32-bit
 // raw data format). Loads at offsets >= bytes return zeros.
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t att_rsrc(const float *base, uint32_t bytes) {
@@ -209,6 +232,7 @@ void attention_kernel(const AttGroup g) {
         constexpr bool MASK = decltype(mask_tag)::value;
         // S^T - mb for keys [key0, key0+32) (s0) and [key0+32, key0+64) (s1).
         floatx16 s0, s1;
+        att_prio(1);
 #pragma unroll
         for (int c = 0; c < 8; ++c) {
             const float4 ka = lds4(&Ks[buf][j][32 * half + 4 * c]);
@@ -231,6 +255,7 @@ void attention_kernel(const AttGroup g) {
                 if (kk + 32 >= n_k) s1[r] = -INFINITY;
             }
         }
+        att_prio(0);
         float mloc = fmaxf(s0[0], s1[0]);
 #pragma unroll
         for (int r = 1; r < 16; ++r) mloc = fmaxf(mloc, fmaxf(s0[r], s1[r]));
@@ -261,6 +286,7 @@ void attention_kernel(const AttGroup g) {
         }
         lsum += __shfl_xor(lsum, 32, 64);
         l_run += lsum;
+        att_prio(1);
         // O^T += V^T P^T, contracting keys in the order the score registers
         // hold them: registers 4a..4a+3 are keys 8a + 4*half + 0..3.
 #pragma unroll
@@ -282,6 +308,7 @@ void attention_kernel(const AttGroup g) {
                 o1 = __builtin_amdgcn_mfma_f32_32x32x2f32(w1v[e], s1[4 * a + e], o1, 0, 0, 0);
             }
         }
+        att_prio(0);
     };
 
     const int tiles = (n_k + ATT_KT - 1) / ATT_KT;
