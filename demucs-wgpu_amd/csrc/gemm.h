@@ -564,10 +564,16 @@ __global__ __launch_bounds__(GEMM_THREADS) __attribute__((amdgpu_waves_per_eu(DM
         lds_wait(a[0], b[0]);
         read_group(1);
         pin_regs(a[0], b[0]);  // keeps group 0's MFMAs behind group 1's reads
+#ifdef DMX_DMA_SETPRIO  // tuning builds only
+        __builtin_amdgcn_s_setprio(1);
+#endif
         mfma_group(0);
         __builtin_amdgcn_sched_barrier(0);  // ... and group 1's wait behind group 0's MFMAs
         lds_wait(a[1], b[1]);
         mfma_group(1);
+#ifdef DMX_DMA_SETPRIO
+        __builtin_amdgcn_s_setprio(0);
+#endif
     }
 
     if (m0 + BM <= M && n0 + BN <= N) {
