@@ -77,7 +77,7 @@ __device__ __forceinline__ void att_prio_imm() {
 __device__ __forceinline__ void att_prio(int p) {
 #if DMX_ATT_SETPRIO
     if (p)
-        att_prio_imm<1>();
+        att_prio_imm<DMX_ATT_SETPRIO>();
     else
         att_prio_imm<0>();
 #else
