@@ -257,7 +257,8 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py: this build runs on one GPU only; multi-GPU runs are not part of it "
-              "(the path would shard by chunk ranges, see DESIGN.md)", file=sys.stderr)
+              "(the path would shard by chunk ranges: each GPU a contiguous run of chunks, "
+              "exchanging its overlap-add halo with its neighbour)", file=sys.stderr)
         sys.exit(2)
 
     import torch
