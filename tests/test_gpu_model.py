@@ -125,6 +125,22 @@ def test_separation_matches_oracle(dmx, oracle, small, shifts, group, progress):
         assert all(a.done <= b.done for a, b in zip(seen, seen[1:]))
 
 
+@pytest.mark.parametrize("group", [1, 2])
+def test_two_lane_schedule_matches_one_lane(dmx, small, group):
+    """The same separation with one stream pair (a progress callback makes
+    the host wait per group) and with alternating pairs, the second pair's
+    group starting when the first reaches its transformer: the stems agree to
+    the f64 atomics' summation order (far tighter than the 60 dB parity
+    gate), so no buffer is reused or read across the lanes too early."""
+    cfg, weights, runner, model = small
+    mix = dmx.signals.synthetic_mix(13, 1.6)
+    opts = dmx.SeparateOptions(shifts=0, overlap=0.25, batch_chunks=group)
+    one = dmx.separate_runners([runner], mix[0], mix[1], 44100, opts, on_progress=lambda p: None)
+    two = dmx.separate_runners([runner], mix[0], mix[1], 44100, opts)
+    for s in range(4):
+        assert snr_db(one[s], two[s]) >= 120.0, (s, snr_db(one[s], two[s]))
+
+
 def test_bag_and_stem_selection_match_oracle(dmx, oracle):
     """A two-network bag with a non-identity weight matrix, then only one stem
     requested (StemSelection::Some): the networks that contribute nothing are
