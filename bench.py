@@ -3,17 +3,20 @@
 Workload ("config 3"): full htdemucs separation of a
 60 s stereo 44.1 kHz synthetic mix, fp32, random-init weights (seed 0), 7.8 s
 segments at overlap 0.25 batched 8 chunks per launch, shifts = 0. One step =
-one separation of the whole mix with the mix already resident in HBM and the
-stems written to HBM (device entry point dmx_separate_device).
+one separation from host f32 samples in to host f32 stems out (dmx_separate:
+the mix upload, the chunk loop on the GPU and the stem readback are all inside
+the clock, as the metric defines it).
 value = x-realtime = audio seconds / wall seconds over the timed steps.
 
-Also reported: the cross-attention kernel's TFLOP/s at the model's shape
-(Q 2688 vs K/V 1344 and Q 1344 vs K/V 2688, a cross layer's two directions,
-in one launch; 8 heads x 64, batch 8) and its roofline
-fraction against the fp32 MFMA peak, measured with HIP events on the launch
-stream; and the
-restated reference CPU backend (oracle/) timed on this host on one 7.8 s
-segment.
+Beside it: the same separation with mix and stems resident in HBM
+(dmx_separate_device); the same workload driven through the SegmentForward
+entry points (dmx_forward_start / collect, one group queued ahead, the chunk
+loop on the host as the reference's pipeline runs it); the cross-attention
+kernel's TFLOP/s at the model's shape (Q 2688 vs K/V 1344 and Q 1344 vs K/V
+2688, a cross layer's two directions, in one launch; 8 heads x 64, batch 8)
+and its roofline fraction against the fp32 MFMA peak, measured with HIP events
+on the launch stream; and the restated reference CPU backend (oracle/) timed
+on this host on the same config-3 separation.
 """
 import argparse
 import ctypes
@@ -79,18 +82,30 @@ def attention_roofline(pkg, torch, batch: int, iters: int):
 
 
 TRAFFIC_SUMMARY = ROOT / "profiles" / "attention_cross_b8_traffic.md"
+ATTENTION_SOURCE = PACKAGE_DIR / "csrc" / "attention.hip"
 
 
 def measured_traffic():
-    """HBM bytes per launch of the roofline kernel, from the committed
-    rocprofv3 FETCH_SIZE / WRITE_SIZE summary (copy-kernel calibrated), or None."""
+    """HBM bytes per launch of the roofline kernel from the committed
+    rocprofv3 FETCH_SIZE / WRITE_SIZE summary (copy-kernel calibrated), with
+    where it comes from. The summary records the sha256 of the kernel source
+    it measured; when attention.hip has changed since, the figure is stale and
+    the traffic is reported as null."""
+    import hashlib
+    fields = {}
     try:
         for line in TRAFFIC_SUMMARY.read_text().splitlines():
-            if line.startswith("traffic_bytes_per_launch:"):
-                return int(line.split(":", 1)[1].strip())
+            if ":" in line and not line.startswith((" ", "|", "#")):
+                k, v = line.split(":", 1)
+                fields[k.strip()] = v.strip()
     except OSError:
-        pass
-    return None
+        return None, "no traffic summary"
+    current = hashlib.sha256(ATTENTION_SOURCE.read_bytes()).hexdigest()
+    if fields.get("source_sha256") != current:
+        return None, f"{TRAFFIC_SUMMARY.name} measured another attention.hip (sha256 {fields.get('source_sha256')})"
+    return int(fields["traffic_bytes_per_launch"]), (
+        f"{TRAFFIC_SUMMARY.relative_to(ROOT)}: rocprofv3 FETCH_SIZE + WRITE_SIZE per dispatch, scaled by a 256 MiB "
+        f"copy's counters; measured on attention.hip sha256 {current[:16]}, the source built here")
 
 
 def copy_calibration(torch, mib: int = 256, iters: int = 5):
@@ -217,28 +232,126 @@ def config5_bf16(pkg, torch, batch=32, iters=3, check=2):
             "dtype": "bf16 MFMA inputs, f32 accumulate/softmax/norms/output"}
 
 
-def cpu_baseline(pkg, seconds_budget: float = 20.0):
-    """The restated reference CPU backend on one 7.8 s segment (config 1):
-    1 warm-up, then the median of up to 3 timed forwards within the budget."""
+def host_cpu():
+    """(threads the oracle may use, model name) of this host."""
+    model = "unknown"
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return os.cpu_count(), model
+
+
+def cpu_baseline(pkg, seconds: float, batch_chunks: int, repeats: int = 3):
+    """The restated reference CPU backend (oracle/, OpenMP on every host core)
+    on the headline workload: the config-3 separation of the same mix with
+    the same weights, after one warm-up forward; median of `repeats`. One
+    7.8 s segment forward (config 1) is timed beside it."""
     sys.path.insert(0, str(ROOT))
     from oracle import binding as oracle
     cfg = pkg.Config()
     weights = pkg.random_init(0, cfg)
-    mix = pkg.signals.gaussian_segments(0, 1, cfg.training_length)
     model = oracle.Model(weights, cfg)
-    t0 = time.perf_counter()
-    model.forward(mix)
-    first = time.perf_counter() - t0
+    seg = pkg.signals.gaussian_segments(0, 1, cfg.training_length)
+    model.forward(seg)  # warm-up: threads, pages, caches
+    mix = pkg.signals.synthetic_mix(0, seconds)
+    opts = pkg.SeparateOptions(shifts=0, overlap=0.25, batch_chunks=batch_chunks)
     times = []
-    while len(times) < 3 and (sum(times) + first) < seconds_budget:
+    for _ in range(repeats):
         t0 = time.perf_counter()
-        model.forward(mix)
+        oracle.separate([model], mix[0], mix[1], cfg.samplerate, opts)
         times.append(time.perf_counter() - t0)
-    t = float(np.median(times)) if times else first
+    t = float(np.median(times))
+    t0 = time.perf_counter()
+    model.forward(seg)
+    t1 = time.perf_counter() - t0
     seg_s = cfg.training_length / cfg.samplerate
-    return {"value": round(seg_s / t, 4), "unit": "x-realtime", "cores": oracle.threads(), "kind": "port",
-            "sample": f"one {seg_s:.1f} s segment forward (config 1), median of {max(1, len(times))} after 1 warm-up; "
-                      f"{t:.2f} s per forward"}
+    nproc, cpu_model = host_cpu()
+    return {"value": round(seconds / t, 4), "unit": "x-realtime", "cores": oracle.threads(), "kind": "port",
+            "sample": f"config 3: separation of the {seconds:g} s mix (11 chunks of 7.8 s, groups of {batch_chunks}), "
+                      f"restated reference CPU backend, median of {repeats} after a warm-up forward: {t:.2f} s each",
+            "host": {"nproc": nproc, "cpu_model": cpu_model},
+            "config1_forward": {"x_realtime": round(seg_s / t1, 4), "s": round(t1, 3)}}
+
+
+def segment_forward_path(pkg, runner, mix, batch_chunks: int, ref_stems, repeats: int = 3):
+    """Config 3 driven through SegmentForward (dmx_forward_start / collect), as
+    the reference's pipeline drives its runner (crates/demucs-core/src/demucs/
+    pipeline.rs:380-515, :584-619; streaming.rs:296-400): the host normalises
+    the mix, cuts centred zero-padded chunks, queues group n + 1 before it
+    collects group n, and overlap-adds on the host (numpy here). Returns the
+    best of `repeats` and the SNR of its stems against dmx_separate's."""
+    cfg = runner.config
+    seg = cfg.training_length
+    stride = int(0.75 * seg)
+    samples = mix.shape[1]
+    half = seg // 2
+    weight = np.concatenate([np.arange(1, half + 1), np.arange(seg - half, 0, -1)]).astype(np.float32)
+    weight /= max(float(weight.max()), 1.0)
+    ref = (mix[0].astype(np.float64) + mix[1]) / 2.0
+    mean = np.float32(ref.mean())
+    std = np.float32(np.sqrt(ref.var(ddof=1))) + np.float32(1e-8)
+    starts = list(range(0, samples, stride))
+
+    def run():
+        norm = (mix - mean) / std
+        acc = np.zeros((cfg.sources, 2, samples), np.float32)
+        sum_w = np.zeros(samples, np.float32)
+        groups = [starts[i:i + batch_chunks] for i in range(0, len(starts), batch_chunks)]
+        in_calls = 0.0
+
+        def chunks(g):
+            x = np.zeros((len(g), 2, seg), np.float32)
+            for j, s0 in enumerate(g):
+                n = min(samples - s0, seg)
+                off = (seg - n) // 2
+                lo = s0 - off
+                a, b = max(lo, 0), min(lo + seg, samples)
+                x[j, :, a - lo:b - lo] = norm[:, a:b]
+            return x
+
+        t0 = time.perf_counter()
+        pending = runner.start(chunks(groups[0]))
+        in_calls += time.perf_counter() - t0
+        for gi, g in enumerate(groups):
+            nxt = None
+            if gi + 1 < len(groups):
+                x = chunks(groups[gi + 1])
+                t1 = time.perf_counter()
+                nxt = runner.start(x)
+                in_calls += time.perf_counter() - t1
+            t1 = time.perf_counter()
+            out = runner.collect(pending)
+            in_calls += time.perf_counter() - t1
+            for j, s0 in enumerate(g):
+                n = min(samples - s0, seg)
+                trim = (seg - n) // 2
+                acc[:, :, s0:s0 + n] += weight[:n] * out[j, :, :, trim:trim + n]
+                sum_w[s0:s0 + n] += weight[:n]
+            pending = nxt
+        stems = acc / sum_w * std + mean
+        return stems, in_calls
+
+    run()
+    best = None
+    for _ in range(repeats):
+        t0 = time.perf_counter()
+        stems, in_calls = run()
+        wall = time.perf_counter() - t0
+        if best is None or wall < best[0]:
+            best = (wall, in_calls)
+    err = stems.astype(np.float64) - ref_stems
+    snr = 10.0 * np.log10(np.sum(ref_stems.astype(np.float64) ** 2) / max(float(np.sum(err * err)), 1e-30))
+    audio_s = samples / cfg.samplerate
+    return {"x_realtime": round(audio_s / best[0], 2), "ms": round(1000.0 * best[0], 2),
+            "ms_in_start_collect": round(1000.0 * best[1], 2),
+            "snr_db_vs_dmx_separate": round(float(snr), 1),
+            "note": f"{len(starts)} chunks in groups of {batch_chunks}, group n+1 started before group n is "
+                    "collected; normalisation, chunking and overlap-add in numpy on the host; best of "
+                    f"{repeats} after a warm-up"}
 
 
 def main():
@@ -275,18 +388,14 @@ def main():
     runner = pkg.Runner(weights, cfg, device=0)
     mix = pkg.signals.synthetic_mix(0, args.seconds)
     samples = mix.shape[1]
-    d_mix = torch.from_numpy(mix).cuda()
-    d_stems = torch.empty((cfg.sources, 2, samples), device="cuda")
-    opts = pkg.SeparateOptions(shifts=0, overlap=0.25, batch_chunks=args.batch_chunks).to_c()
-    lib = pkg._native.load()
-    handles = (ctypes.c_void_p * 1)(runner.handle)
+    audio_s = samples / cfg.samplerate
+    opts = pkg.SeparateOptions(shifts=0, overlap=0.25, batch_chunks=args.batch_chunks)
+    left, right = np.ascontiguousarray(mix[0]), np.ascontiguousarray(mix[1])
 
+    # The metric: host f32 mix in, host f32 stems out, one fresh output array
+    # per call as a caller of Demucs::separate gets.
     def step():
-        rc = lib.dmx_separate_device(handles, None, 1, None, ctypes.c_void_p(d_mix.data_ptr()), samples,
-                                     cfg.samplerate, ctypes.byref(opts), pkg._native.PROGRESS(), None,
-                                     ctypes.c_void_p(d_stems.data_ptr()))
-        if rc != 0:
-            raise RuntimeError(pkg._native.last_error())
+        return pkg.separate_runners([runner], left, right, cfg.samplerate, opts)
 
     for _ in range(args.warmup):
         step()
@@ -294,32 +403,57 @@ def main():
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for _ in range(args.steps):
-        step()
+        stems = step()
     runner.synchronize()
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t0
     ms_per_step = 1000.0 * elapsed / args.steps
-    audio_s = samples / cfg.samplerate
     xrt = audio_s * args.steps / elapsed
-    if not np.isfinite(d_stems.abs().sum().item()):
+    if not np.isfinite(stems).all():
         raise RuntimeError("non-finite stems")
 
-    # The same separation from host arrays to host stems (dmx_separate: the
-    # mix upload and the stem readback are inside the timing), after one
-    # untimed run. Reported beside `value`, never as it.
-    host_opts = pkg.SeparateOptions(shifts=0, overlap=0.25, batch_chunks=args.batch_chunks)
-    left, right = np.ascontiguousarray(mix[0]), np.ascontiguousarray(mix[1])
-    pkg.separate_runners([runner], left, right, cfg.samplerate, host_opts)
+    # The same separation with the mix and the stems resident in HBM
+    # (dmx_separate_device), over the same number of steps.
+    d_mix = torch.from_numpy(mix).cuda()
+    d_stems = torch.empty((cfg.sources, 2, samples), device="cuda")
+    c_opts = opts.to_c()
+    lib = pkg._native.load()
+    handles = (ctypes.c_void_p * 1)(runner.handle)
+
+    def device_step():
+        rc = lib.dmx_separate_device(handles, None, 1, None, ctypes.c_void_p(d_mix.data_ptr()), samples,
+                                     cfg.samplerate, ctypes.byref(c_opts), pkg._native.PROGRESS(), None,
+                                     ctypes.c_void_p(d_stems.data_ptr()))
+        if rc != 0:
+            raise RuntimeError(pkg._native.last_error())
+
+    for _ in range(max(1, args.warmup)):
+        device_step()
+    runner.synchronize()
+    torch.cuda.synchronize()
     t0 = time.perf_counter()
-    pkg.separate_runners([runner], left, right, cfg.samplerate, host_opts)
-    host_s = time.perf_counter() - t0
-    host_io = {"x_realtime": round(audio_s / host_s, 2), "ms": round(1000.0 * host_s, 2),
-               "note": "host f32 mix in, host f32 stems out (dmx_separate); one run after a warm-up"}
+    for _ in range(args.steps):
+        device_step()
+    runner.synchronize()
+    torch.cuda.synchronize()
+    dev_s = (time.perf_counter() - t0) / args.steps
+    dev_stems = d_stems.cpu().numpy()
+    dev_snr = min(10.0 * np.log10(np.sum(dev_stems[i].astype(np.float64) ** 2) /
+                                  max(float(np.sum((dev_stems[i].astype(np.float64) - stems[i]) ** 2)), 1e-30))
+                  for i in range(cfg.sources))
+    device_resident = {"x_realtime": round(audio_s / dev_s, 2), "ms": round(1000.0 * dev_s, 2),
+                       "min_stem_snr_db_vs_value_run": round(float(dev_snr), 1),
+                       "note": "mix and stems resident in HBM (dmx_separate_device), mean over the same steps"}
+    del d_mix, d_stems
+
+    segment_forward = segment_forward_path(pkg, runner, mix, args.batch_chunks, stems)
 
     attn_ms, attn_flops = attention_roofline(pkg, torch, args.batch_chunks, args.attn_iters)
     attn_tflops = attn_flops / (attn_ms * 1e-3) / 1e12
+    traffic, traffic_source = measured_traffic()
     roofline = {"bound": "mfma", "achieved": round(attn_tflops, 2), "peak": FP32_MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
-                "frac": round(attn_tflops / FP32_MFMA_PEAK_TFLOPS, 4), "traffic": measured_traffic(),
+                "frac": round(attn_tflops / FP32_MFMA_PEAK_TFLOPS, 4), "traffic": traffic,
+                "traffic_source": traffic_source,
                 "kernel": "attention_kernel (fused cross-attention, fp32 MFMA)",
                 "per_launch": f"sum of 4*B*Lq*Lk*512 flops over (Lq, Lk) = (2688, 1344) and (1344, 2688), "
                               f"B={args.batch_chunks}, both directions in one launch (dmx_op_attention_pair); "
@@ -339,12 +473,13 @@ def main():
         "data": "synthetic (seeded 60 s mix: 16 sinusoids + pink noise + decaying bursts; random-init seed-0 weights)",
         "config": {"workload": f"config 3: htdemucs separation of a {args.seconds:g} s stereo mix, 7.8 s segments, "
                                f"overlap 0.25, {args.batch_chunks} chunks per launch, shifts=0, fp32, "
-                               "mix and stems resident in HBM",
+                               "host f32 mix in to host f32 stems out (dmx_separate)",
                    "segment_samples": cfg.training_length, "batch_chunks": args.batch_chunks},
         "cross_attn_tflops": round(attn_tflops, 2),
-        "host_io": host_io,
+        "device_resident": device_resident,
+        "segment_forward": segment_forward,
         "roofline": roofline,
-        "cpu_baseline": None if args.no_cpu_baseline else cpu_baseline(pkg),
+        "cpu_baseline": None if args.no_cpu_baseline else cpu_baseline(pkg, args.seconds, args.batch_chunks),
     }
     if not args.no_other_configs:
         del runner

@@ -334,7 +334,7 @@ class Demucs:
         return self.runners[0].forward(mix)
 
     def separate(self, left, right, sample_rate: int) -> List[Stem]:
-        return self.separate_with_progress(left, right, sample_rate, lambda p: None)
+        return self.separate_with_options(left, right, sample_rate, SeparateOptions())
 
     def separate_with_progress(self, left, right, sample_rate: int,
                                on_progress: Callable[[SeparationProgress], None]) -> List[Stem]:

@@ -11,7 +11,7 @@ namespace dmx {
 
 enum Act { ACT_NONE = 0, ACT_GELU = 1 };
 
-// ---------------- GEMM-based ops (conv.cu / linear.cu) ----------------
+// ---------------- GEMM-based ops (conv.hip, gemm.h) ----------------
 
 // Convolution weights in GEMM order. A PyTorch (oc, ic, kh, kw) weight is
 // consumed in channel quads whenever conv_tap_major(ic, kh, kw): the
@@ -117,7 +117,7 @@ void linear(hipStream_t s, const float *x, int64_t ldx, int64_t x_batch_stride, 
 void tokens_to_channels(hipStream_t s, const float *tok, int b, int F, int T, int D, const float *w, const float *bias,
                         int M, float *out);
 
-// ---------------- attention (attention.cu) ----------------
+// ---------------- attention (attention.hip) ----------------
 // Fused softmax(q k^T * scale) v per (batch, head); q/k/v/out are token-major
 // with the head's 64 lanes at column h*64 of rows of stride ld*.
 void attention(hipStream_t s, const float *q, int64_t ldq, const float *k, int64_t ldk, const float *v, int64_t ldv,
@@ -139,7 +139,7 @@ struct AttentionArgs {
 };
 void attention_grouped(hipStream_t s, const AttentionArgs *probs, int count, float scale);
 
-// ---------------- norms / elementwise (norm.cu) ----------------
+// ---------------- norms / elementwise (norm.hip) ----------------
 void layer_norm_rows(hipStream_t s, const float *x, int rows, int dim, const float *w, const float *b, float *out,
                      const float *add, int add_rows);
 // (b, c, positions) channel-major -> token rows (b, T*F, c) reordered token = t*F + f,
@@ -160,7 +160,7 @@ void zero_floats(hipStream_t s, float *p, int64_t n);
 void copy_rows(hipStream_t s, const float *src, int64_t rows, int64_t src_ld, int64_t n_copy, float *dst,
                int64_t dst_len);
 
-// ---------------- spectral / framing (spectral.cu) ----------------
+// ---------------- spectral / framing (spectral.hip) ----------------
 // _spec + pack (CaC) + per-batch normalisation of both branches:
 // mix (b, 2, L) -> xspec (b, 4, nfft/2, le) normalised, xwave (b, 2, L) normalised,
 // norms[4*b] = (mean, std, mean_t, std_t) per batch (f32).
@@ -175,15 +175,16 @@ void stft_cac_raw(hipStream_t s, const float *mix, int b, int L, int nfft, float
                   const float *twiddles);
 void make_twiddles(int nfft, float *host_out);  // nfft/2 complex (cos, -sin) pairs
 
-// ---------------- chunking / overlap-add (pipeline.cu) ----------------
+// ---------------- chunking / overlap-add (pipeline.hip) ----------------
 void mix_moments(hipStream_t s, const float *mix, int64_t samples, double *stats);
 void build_chunks(hipStream_t s, const float *mix, int64_t mix_len, const double *stats, int group, const int64_t *starts,
                   const int64_t *lengths, int64_t seg, int64_t view_len, int64_t shift_offset, int64_t max_shift,
                   float *out);
 void ola_accumulate(hipStream_t s, const float *chunk_out, int group, const int64_t *starts, const int64_t *lengths,
                     int64_t seg, int rows, int64_t view_len, const float *weight, float *acc, float *sum_w);
+// Finishes output samples [lo, hi) of every row from the pass's sums (modes in pipeline.hip).
 void ola_finish(hipStream_t s, const float *acc, const float *sum_w, int rows, int64_t view_len, int64_t trim,
-                int64_t samples, const double *stats, float scale, int accumulate, float *stems,
+                int64_t lo, int64_t hi, int64_t samples, const double *stats, float scale, int mode, float *stems,
                 const uint8_t *row_mask);
 void bag_accumulate(hipStream_t s, const float *net_out, int64_t group_batch, int sources, int64_t per_source,
                     const float *weights, float *combined, int first);

@@ -90,31 +90,32 @@ __global__ __launch_bounds__(256) void ola_accumulate_kernel(const float *__rest
     }
 }
 
-// frame = acc / sum_w at view index t + trim; then either
-//   mode 0: stems = (frame * scale) * std + mean
-//   mode 1: stems += frame             (one shift pass of several)
-//   mode 2: stems = (stems * scale) * std + mean   (after the last pass)
+// Output samples t in [lo, hi): frame = acc / sum_w at view index t + trim;
+// then either
+//   mode 0: stems = (frame * scale) * std + mean           (the only pass)
+//   mode 1: stems += frame                                 (a pass of several, not the last)
+//   mode 2: stems = ((stems + frame) * scale) * std + mean (the last pass of several)
+// which rounds as the reference's sum over passes, * 1/shifts, * std + mean.
 __global__ __launch_bounds__(256) void ola_finish_kernel(const float *__restrict__ acc, const float *__restrict__ sum_w,
-                                                         int64_t view_len, int64_t trim, int64_t samples,
-                                                         const double *__restrict__ stats, int64_t mix_len, float scale,
-                                                         int mode, float *__restrict__ stems,
+                                                         int64_t view_len, int64_t trim, int64_t lo, int64_t hi,
+                                                         int64_t samples, const double *__restrict__ stats,
+                                                         int64_t mix_len, float scale, int mode,
+                                                         float *__restrict__ stems,
                                                          const uint8_t *__restrict__ row_mask, int channels) {
     const int r = blockIdx.y;
     if (row_mask && !row_mask[r / channels]) return;
     float mean, stdv;
     global_norm(stats, mix_len, mean, stdv);
-    for (int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x; t < samples; t += (int64_t)gridDim.x * 256) {
+    for (int64_t t = lo + (int64_t)blockIdx.x * 256 + threadIdx.x; t < hi; t += (int64_t)gridDim.x * 256) {
         float *dst = stems + (int64_t)r * samples + t;
-        if (mode == 2) {
-            *dst = (*dst * scale) * stdv + mean;
-            continue;
-        }
         int64_t tv = t + trim;
         float frame = acc[(int64_t)r * view_len + tv] / sum_w[tv];
         if (mode == 0)
             *dst = (frame * scale) * stdv + mean;
-        else
+        else if (mode == 1)
             *dst += frame;
+        else
+            *dst = ((*dst + frame) * scale) * stdv + mean;
     }
 }
 
@@ -187,10 +188,15 @@ void ola_accumulate(hipStream_t s, const float *chunk_out, int group, const int6
 }
 
 void ola_finish(hipStream_t s, const float *acc, const float *sum_w, int rows, int64_t view_len, int64_t trim,
-                int64_t samples, const double *stats, float scale, int mode, float *stems, const uint8_t *row_mask) {
+                int64_t lo, int64_t hi, int64_t samples, const double *stats, float scale, int mode, float *stems,
+                const uint8_t *row_mask) {
     // `stats` are the mix moments; samples is the mix length they were taken over.
-    hipLaunchKernelGGL(ola_finish_kernel, dim3(gcap(samples, 2048), (unsigned)rows), dim3(256), 0, s, acc, sum_w,
-                       view_len, trim, samples, stats, samples, scale, mode, stems, row_mask, 2);
+    require_ptrs({acc, sum_w, stats, stems}, "ola_finish");
+    DMX_REQUIRE(mode >= 0 && mode <= 2, "ola_finish: unknown mode");
+    DMX_REQUIRE(0 <= lo && lo <= hi && hi <= samples && hi + trim <= view_len, "ola_finish: range outside the view");
+    if (hi == lo) return;
+    hipLaunchKernelGGL(ola_finish_kernel, dim3(gcap(hi - lo, 2048), (unsigned)rows), dim3(256), 0, s, acc, sum_w,
+                       view_len, trim, lo, hi, samples, stats, samples, scale, mode, stems, row_mask, 2);
     DMX_LAUNCH_CHECK();
 }
 

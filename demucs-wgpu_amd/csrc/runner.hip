@@ -14,6 +14,7 @@
 #include <cmath>
 #include <cstdlib>
 #include <cstring>
+#include <functional>
 #include <map>
 #include <memory>
 #include <mutex>
@@ -23,6 +24,7 @@
 #include "../../include/dmx.h"
 #include "common.h"
 #include "ops.h"
+#include "staging.h"
 
 namespace dmx {
 namespace {
@@ -157,11 +159,24 @@ struct TLayerW {
 }  // namespace
 }  // namespace dmx
 
+namespace dmx {
+namespace {
+// Pinned staging of one SegmentForward group in flight: the caller's mix is
+// copied into `in`, the stems come back into `out`. Slots belong to the
+// runner and are reused; a slot grows only when a larger group comes.
+struct PendingSlot {
+    float *in = nullptr, *out = nullptr;
+    size_t in_cap = 0, out_cap = 0;  // floats
+    hipEvent_t done = nullptr;       // the group's stems are in `out`
+    bool busy = false;
+};
+}  // namespace
+}  // namespace dmx
+
 struct dmx_pending {
-    float *host_in = nullptr;   // pinned staging of the caller's mix
-    float *host_out = nullptr;  // pinned
-    size_t count = 0;
-    hipEvent_t done = nullptr;
+    dmx_runner *runner = nullptr;
+    int slot = -1;
+    size_t count = 0;  // floats of stems
 };
 
 struct dmx_runner {
@@ -193,10 +208,16 @@ struct dmx_runner {
     float *twiddles = nullptr;                      // nfft/2 complex + nfft window
     std::map<std::pair<int64_t, int64_t>, float *> pos2d;  // (freqs, frames) -> (T*F, D)
     std::map<int64_t, float *> pos1d;                       // length -> (L, D)
-    std::map<int64_t, float *> ola_weights;                 // segment -> (seg)
+    std::map<std::pair<int64_t, double>, float *> ola_weights;  // (segment, power) -> (seg)
     std::vector<void *> owned;                              // device blocks freed at destroy
     float *eye = nullptr;                                   // (D, D) identity + D zeros
     dmx::Trace trace;
+    std::vector<hipEvent_t> marks;          // per chunk group of a separation (mark_event)
+    dmx::PinnedBuffer staging;              // dmx_separate's mix and stems in pinned memory
+    dmx::PinnedRing ring;                   // its staging for calls too large for `staging`
+    std::vector<hipEvent_t> xfer;           // per readback block of dmx_separate (xfer_event)
+    std::vector<dmx::PendingSlot> pending;  // staging of dmx_forward_start / collect
+    int next_lane = 0;                      // lane of the next dmx_forward_start
 };
 
 namespace dmx {
@@ -1008,16 +1029,63 @@ struct ShiftRng {
 };
 
 float *ola_weight_for(dmx_runner &r, int64_t seg, double power) {
-    auto it = r.ola_weights.find(seg);
-    if (it != r.ola_weights.end() && power == 1.0) return it->second;
+    auto key = std::make_pair(seg, power);
+    auto it = r.ola_weights.find(key);
+    if (it != r.ola_weights.end()) return it->second;
     float *p = upload(r, transition_weight(seg, power));
-    if (power == 1.0) r.ola_weights[seg] = p;
+    r.ola_weights[key] = p;
     return p;
 }
 
+// The runner's i-th group-mark event, made on first use.
+hipEvent_t mark_event(dmx_runner &r, size_t i) {
+    while (r.marks.size() <= i) {
+        hipEvent_t e = nullptr;
+        DMX_HIP(hipEventCreateWithFlags(&e, hipEventDisableTiming));
+        r.marks.push_back(e);
+    }
+    return r.marks[i];
+}
+
+// The runner's i-th readback event, made on first use.
+hipEvent_t xfer_event(dmx_runner &r, size_t i) {
+    while (r.xfer.size() <= i) {
+        hipEvent_t e = nullptr;
+        DMX_HIP(hipEventCreateWithFlags(&e, hipEventDisableTiming));
+        r.xfer.push_back(e);
+    }
+    return r.xfer[i];
+}
+
+// Largest pinned staging (mix + stems) dmx_separate keeps per runner:
+// DMX_PINNED_MAX_MB (read per call), default 1024, about six minutes of four
+// stereo stems. Larger calls go through the runner's 24 MB ring instead and
+// read the stems back after the last group.
+size_t pinned_limit() {
+    const char *v = std::getenv("DMX_PINNED_MAX_MB");
+    long mb = v ? std::atol(v) : 1024;
+    return (size_t)std::max(0L, mb) << 20;
+}
+
+// What a caller of separate_device can wait for: `ev` is recorded on the
+// runner's main stream after a chunk group's overlap-add; by then `done`
+// chunk forwards have finished and, in the last pass, output samples
+// [lo, hi) of every wanted row are final in `stems`.
+struct GroupMark {
+    hipEvent_t ev;
+    size_t done;
+    int64_t lo, hi;
+};
+
+// The chunk loop on the device; enqueues everything and returns at once.
+// `marks` receives one entry per chunk group, `total` the progress total.
+// `on_final(lo, hi)` (optional) is called while the work is enqueued, right
+// after output samples [lo, hi) are finished on the main stream, so the
+// caller can queue their readback there in order.
 void separate_device(dmx_runner *const *nets, const float *bag_weights, int n_nets, const uint8_t *wanted,
-                     const float *mix, int64_t samples, int sample_rate, const dmx_separate_options &o,
-                     dmx_progress_fn progress, void *user, float *stems) {
+                     const float *mix, int64_t samples, int sample_rate, const dmx_separate_options &o, float *stems,
+                     std::vector<GroupMark> &marks, size_t &total,
+                     const std::function<void(int64_t, int64_t)> &on_final = nullptr) {
     if (n_nets < 1 || !nets || !nets[0]) throw_error(DMX_ERR_ARGUMENT, "no network");
     dmx_runner &r0 = *nets[0];
     for (int i = 0; i < n_nets; ++i) {
@@ -1037,7 +1105,7 @@ void separate_device(dmx_runner *const *nets, const float *bag_weights, int n_ne
     for (int i = 0; i < n_nets; ++i)
         if (seg > nets[i]->training_length) throw_error(DMX_ERR_SHAPE, "segment longer than the model's");
     const int64_t stride = (int64_t)((1.0 - o.overlap) * (double)seg);
-    if (stride == 0) throw_error(DMX_ERR_SHAPE, "overlap leaves a zero stride");
+    if (stride <= 0) throw_error(DMX_ERR_SHAPE, "overlap leaves no stride");
     const int group = std::max(1, std::min(o.batch_chunks, 64));
     std::vector<uint8_t> requested(S, 1);
     if (wanted)
@@ -1073,6 +1141,9 @@ void separate_device(dmx_runner *const *nets, const float *bag_weights, int n_ne
     DMX_HIP(hipMemcpyAsync(d_tot.p, totals.data(), totals.size() * sizeof(float), hipMemcpyHostToDevice, s));
     DBuf d_mask(s, S);
     DMX_HIP(hipMemcpyAsync(d_mask.p, requested.data(), S, hipMemcpyHostToDevice, s));
+    // The three copies above read pageable host vectors that end with this
+    // call; they are small, and a pageable async copy has read its source
+    // when it returns.
 
     DBuf stats = dbuf(s, 2);
     mix_moments(s, mix, samples, stats.d());
@@ -1083,7 +1154,7 @@ void separate_device(dmx_runner *const *nets, const float *bag_weights, int n_ne
     const int passes = std::max(1, shifts);
     // Progress: chunks per pass x passes x active networks.
     auto chunks_in = [&](int64_t view_len) { return (view_len + stride - 1) / stride; };
-    size_t total = 0;
+    total = 0;
     {
         ShiftRng probe(0x5eed1234ULL);
         for (int p = 0; p < passes; ++p) {
@@ -1091,6 +1162,7 @@ void separate_device(dmx_runner *const *nets, const float *bag_weights, int n_ne
             total += (size_t)chunks_in(vl) * active.size();
         }
     }
+    marks.clear();
     size_t done = 0;
     const float scale = shifts > 0 ? 1.0f / (float)shifts : 1.0f;
     if (shifts > 1) {
@@ -1098,7 +1170,12 @@ void separate_device(dmx_runner *const *nets, const float *bag_weights, int n_ne
         for (int i = 0; i < S; ++i)
             if (requested[i]) zero_floats(s, stems + (int64_t)i * 2 * samples, 2 * samples);
     }
+    const uint8_t *row_mask = static_cast<const uint8_t *>(d_mask.p);
     for (int pass = 0; pass < passes; ++pass) {
+        const bool last_pass = pass == passes - 1;
+        // mode of ola_finish (pipeline.hip): the only pass, an earlier pass
+        // of several, or the last of several.
+        const int mode = passes == 1 ? 0 : last_pass ? 2 : 1;
         int64_t offset = 0, view_len = samples, trim = 0, mshift = 0;
         if (shifts > 0) {
             offset = rng.randint(max_shift);
@@ -1113,9 +1190,8 @@ void separate_device(dmx_runner *const *nets, const float *bag_weights, int n_ne
         // (stream_b, side_b), so the forwards of consecutive groups overlap;
         // every overlap-add stays on s in group order. A lane's buffers come
         // from s's pool (taken here, released after the pass) and lane b
-        // waits for s before it reuses them. Progress reports need the
-        // host to wait per group, so they keep one lane.
-        const bool two_lanes = !progress && r0.stream_b && !single_stream_env() && !r0.trace.record;
+        // waits for s before it reuses them.
+        const bool two_lanes = r0.stream_b && !single_stream_env() && !r0.trace.record;
         const int lanes = two_lanes ? 2 : 1;
         std::vector<DBuf> chunk, out, one;
         for (int l = 0; l < lanes; ++l) {
@@ -1136,6 +1212,7 @@ void separate_device(dmx_runner *const *nets, const float *bag_weights, int n_ne
         const int stagger = !two_lanes ? 0 : stag_env ? std::atoi(stag_env) : 1;
         bool mid_marked = false;
         int lane = 0;
+        int64_t finished = 0;  // output samples [0, finished) are final (last pass)
         for (int64_t cursor = 0; cursor < view_len;) {
             std::vector<int64_t> starts, lens;
             while ((int)starts.size() < group && cursor < view_len) {
@@ -1169,20 +1246,29 @@ void separate_device(dmx_runner *const *nets, const float *bag_weights, int n_ne
             ola_accumulate(s, out_p, g, starts.data(), lens.data(), seg, rows, view_len, weight, acc.f(), sum_w.f());
             if (lane) DMX_HIP(hipEventRecord(r0.ev_lane, s));
             done += (size_t)g * active.size();
-            if (progress) {
-                DMX_HIP(hipStreamSynchronize(s));
-                progress(done, total, user);
+            // No later chunk starts before `cursor`, so view samples below it
+            // are final: in the last pass, finish their output samples now,
+            // which lets a caller read them back while later groups compute.
+            GroupMark m{nullptr, done, finished, finished};
+            if (last_pass) {
+                const int64_t hi = cursor < view_len ? std::min(samples, std::max<int64_t>(0, cursor - trim)) : samples;
+                if (hi > finished) {
+                    ola_finish(s, acc.f(), sum_w.f(), rows, view_len, trim, finished, hi, samples, stats.d(), scale,
+                               mode, stems, row_mask);
+                    if (on_final) on_final(finished, hi);
+                    m.hi = finished = hi;
+                }
             }
+            m.ev = mark_event(r0, marks.size());
+            DMX_HIP(hipEventRecord(m.ev, s));
+            marks.push_back(m);
             lane = (lane + 1) % lanes;
         }
         r0.mark_mid = 0;
-        const int mode = shifts > 1 ? 1 : 0;
-        ola_finish(s, acc.f(), sum_w.f(), rows, view_len, trim, samples, stats.d(), scale, mode, stems,
-                   static_cast<const uint8_t *>(d_mask.p));
+        if (!last_pass)
+            ola_finish(s, acc.f(), sum_w.f(), rows, view_len, trim, 0, samples, samples, stats.d(), scale, mode, stems,
+                       row_mask);
     }
-    if (shifts > 1)
-        ola_finish(s, nullptr, nullptr, rows, 0, 0, samples, stats.d(), scale, 2, stems,
-                   static_cast<const uint8_t *>(d_mask.p));
 }
 
 }  // namespace
@@ -1296,6 +1382,13 @@ void dmx_runner_destroy(dmx_runner *r) {
     for (void *p : r->owned) (void)hipFree(p);
     for (hipEvent_t e : {r->ev_fork, r->ev_join, r->ev_lane, r->ev_mid})
         if (e) (void)hipEventDestroy(e);
+    for (hipEvent_t e : r->marks) (void)hipEventDestroy(e);
+    for (hipEvent_t e : r->xfer) (void)hipEventDestroy(e);
+    for (PendingSlot &sl : r->pending) {
+        if (sl.done) (void)hipEventDestroy(sl.done);
+        if (sl.in) (void)hipHostFree(sl.in);
+        if (sl.out) (void)hipHostFree(sl.out);
+    }
     for (hipStream_t st : {r->side, r->stream_b, r->side_b, r->stream})
         if (st) (void)hipStreamDestroy(st);
     delete r;
@@ -1308,7 +1401,9 @@ int dmx_synchronize(dmx_runner *r) {
     return guarded([&] {
         if (!r) throw_error(DMX_ERR_ARGUMENT, "null runner");
         set_device(r);
-        DMX_HIP(hipStreamSynchronize(r->stream));
+        // dmx_forward_start may have queued a group on the second lane.
+        for (hipStream_t st : {r->stream, r->side, r->stream_b, r->side_b})
+            if (st) DMX_HIP(hipStreamSynchronize(st));
     });
 }
 
@@ -1331,53 +1426,82 @@ int dmx_forward_device(dmx_runner *r, const float *d_mix, int64_t batch, int64_t
 int dmx_forward_start(dmx_runner *r, const float *mix, int64_t batch, int64_t channels, int64_t length,
                       dmx_pending **out) {
     if (out) *out = nullptr;
-    std::unique_ptr<dmx_pending> p(new dmx_pending());
-    int rc = guarded([&] {
+    return guarded([&] {
         if (!r || !mix || !out) throw_error(DMX_ERR_ARGUMENT, "null argument");
         set_device(r);
         if (channels != r->cfg.audio_channels) throw_error(DMX_ERR_SHAPE, "wrong audio channel count");
         if (batch <= 0 || length <= 0 || length > r->training_length)
             throw_error(DMX_ERR_SHAPE, "input must hold 1..training_length samples per channel");
-        hipStream_t s = r->stream;
         const size_t in_n = (size_t)(batch * channels * length);
         const size_t out_n = (size_t)(batch * r->cfg.sources * channels * length);
-        DMX_HIP(hipHostMalloc((void **)&p->host_in, in_n * sizeof(float), hipHostMallocDefault));
-        std::memcpy(p->host_in, mix, in_n * sizeof(float));
-        DMX_HIP(hipHostMalloc((void **)&p->host_out, out_n * sizeof(float), hipHostMallocDefault));
-        p->count = out_n;
-        DBuf d_in(s, in_n * sizeof(float)), d_out(s, out_n * sizeof(float));
-        DMX_HIP(hipMemcpyAsync(d_in.p, p->host_in, in_n * sizeof(float), hipMemcpyHostToDevice, s));
-        forward_device(*r, s, d_in.f(), batch, channels, length, d_out.f());
-        DMX_HIP(hipMemcpyAsync(p->host_out, d_out.p, out_n * sizeof(float), hipMemcpyDeviceToHost, s));
-        DMX_HIP(hipEventCreateWithFlags(&p->done, hipEventDisableTiming));
-        DMX_HIP(hipEventRecord(p->done, s));
-        // Both staging buffers belong to the pending group until collect.
+        // A free staging slot: one that is large enough, else any free one
+        // (grown), else a new one. Two groups in flight use two slots.
+        int k = -1;
+        for (int i = 0; i < (int)r->pending.size() && k < 0; ++i)
+            if (!r->pending[i].busy && r->pending[i].in_cap >= in_n && r->pending[i].out_cap >= out_n) k = i;
+        for (int i = 0; i < (int)r->pending.size() && k < 0; ++i)
+            if (!r->pending[i].busy) k = i;
+        if (k < 0) {
+            r->pending.emplace_back();
+            k = (int)r->pending.size() - 1;
+            DMX_HIP(hipEventCreateWithFlags(&r->pending[k].done, hipEventDisableTiming));
+        }
+        PendingSlot &sl = r->pending[k];
+        if (sl.in_cap < in_n) {
+            if (sl.in) DMX_HIP(hipHostFree(sl.in));
+            sl.in = nullptr;
+            sl.in_cap = 0;
+            DMX_HIP(hipHostMalloc((void **)&sl.in, in_n * sizeof(float), hipHostMallocDefault));
+            sl.in_cap = in_n;
+        }
+        if (sl.out_cap < out_n) {
+            if (sl.out) DMX_HIP(hipHostFree(sl.out));
+            sl.out = nullptr;
+            sl.out_cap = 0;
+            DMX_HIP(hipHostMalloc((void **)&sl.out, out_n * sizeof(float), hipHostMallocDefault));
+            sl.out_cap = out_n;
+        }
+        // Consecutive groups alternate between the two stream pairs, so the
+        // group queued ahead runs beside the one being collected.
+        const bool two_lanes = r->stream_b && !r->trace.record && !single_stream_env();
+        hipStream_t ls = two_lanes && (r->next_lane++ & 1) ? r->stream_b : r->stream;
+        host_copy(sl.in, mix, in_n * sizeof(float));
+        try {
+            DBuf d_in(ls, in_n * sizeof(float)), d_out(ls, out_n * sizeof(float));
+            DMX_HIP(hipMemcpyAsync(d_in.p, sl.in, in_n * sizeof(float), hipMemcpyHostToDevice, ls));
+            forward_device(*r, ls, d_in.f(), batch, channels, length, d_out.f());
+            DMX_HIP(hipMemcpyAsync(sl.out, d_out.p, out_n * sizeof(float), hipMemcpyDeviceToHost, ls));
+            DMX_HIP(hipEventRecord(sl.done, ls));
+        } catch (...) {
+            // Nothing queued may still read or write the slot once it is free.
+            (void)hipStreamSynchronize(ls);
+            throw;
+        }
+        sl.busy = true;
+        *out = new dmx_pending{r, k, out_n};
     });
-    if (rc != DMX_OK) {
-        if (p->done) (void)hipEventSynchronize(p->done);
-        if (p->host_in) (void)hipHostFree(p->host_in);
-        if (p->host_out) (void)hipHostFree(p->host_out);
-        if (p->done) (void)hipEventDestroy(p->done);
-        return rc;
-    }
-    *out = p.release();
-    return DMX_OK;
 }
 
 int dmx_forward_collect(dmx_runner *r, dmx_pending *p, float *stems) {
-    int rc = guarded([&] {
-        if (!r || !p || !stems) throw_error(DMX_ERR_ARGUMENT, "null argument");
-        set_device(r);
-        DMX_HIP(hipEventSynchronize(p->done));
-        std::memcpy(stems, p->host_out, p->count * sizeof(float));
-    });
-    if (p) {
-        if (p->done) (void)hipEventSynchronize(p->done);
-        if (p->host_in) (void)hipHostFree(p->host_in);
-        if (p->host_out) (void)hipHostFree(p->host_out);
-        if (p->done) (void)hipEventDestroy(p->done);
-        delete p;
+    // An argument error leaves the group pending; any other outcome ends it.
+    if (!r || !p || !stems) {
+        last_error_slot() = "null argument";
+        return DMX_ERR_ARGUMENT;
     }
+    if (p->runner != r) {
+        last_error_slot() = "the pending group belongs to another runner";
+        return DMX_ERR_ARGUMENT;
+    }
+    PendingSlot &sl = r->pending[p->slot];
+    int rc = guarded([&] {
+        set_device(r);
+        DMX_HIP(hipEventSynchronize(sl.done));
+        advise_huge_pages(stems, p->count * sizeof(float));
+        host_copy(stems, sl.out, p->count * sizeof(float));
+    });
+    (void)hipEventSynchronize(sl.done);
+    sl.busy = false;
+    delete p;
     return rc;
 }
 
@@ -1412,21 +1536,32 @@ int dmx_separate_device(dmx_runner *const *nets, const float *bag_weights, int32
                         const float *d_mix, int64_t samples, int32_t sample_rate, const dmx_separate_options *opts,
                         dmx_progress_fn progress, void *user, float *d_stems) {
     return guarded([&] {
-        if (!nets || !d_mix || !d_stems) throw_error(DMX_ERR_ARGUMENT, "null argument");
+        if (!nets || !nets[0] || !d_mix || !d_stems) throw_error(DMX_ERR_ARGUMENT, "null argument");
         dmx_separate_options o;
         dmx_separate_options_default(&o);
         if (opts) o = *opts;
         set_device(nets[0]);
-        separate_device(nets, bag_weights, n_nets, stems_wanted, d_mix, samples, sample_rate, o, progress, user,
-                        d_stems);
+        std::vector<GroupMark> marks;
+        size_t total = 0;
+        separate_device(nets, bag_weights, n_nets, stems_wanted, d_mix, samples, sample_rate, o, d_stems, marks,
+                        total);
+        // Progress comes from the host waiting on each group's mark, so a
+        // callback does not change the schedule on the GPU.
+        if (progress)
+            for (const GroupMark &m : marks) {
+                DMX_HIP(hipEventSynchronize(m.ev));
+                progress(m.done, total, user);
+            }
     });
 }
 
 int dmx_separate(dmx_runner *const *nets, const float *bag_weights, int32_t n_nets, const uint8_t *stems_wanted,
                  const float *left, const float *right, int64_t samples, int32_t sample_rate,
                  const dmx_separate_options *opts, dmx_progress_fn progress, void *user, float *stems_out) {
-    return guarded([&] {
+    std::vector<uint64_t> host_jobs;  // pool jobs that touch the caller's memory
+    int rc = guarded([&] {
         if (!nets || !nets[0] || !left || !right || !stems_out) throw_error(DMX_ERR_ARGUMENT, "null argument");
+        if (samples <= 0) throw_error(DMX_ERR_SHAPE, "empty mix");
         dmx_separate_options o;
         dmx_separate_options_default(&o);
         if (opts) o = *opts;
@@ -1434,18 +1569,117 @@ int dmx_separate(dmx_runner *const *nets, const float *bag_weights, int32_t n_ne
         set_device(&r);
         hipStream_t s = r.stream;
         const int S = r.cfg.sources;
-        DBuf mix = fbuf(s, 2 * samples), stems = fbuf(s, (int64_t)S * 2 * samples);
-        DMX_HIP(hipMemcpyAsync(mix.f(), left, samples * sizeof(float), hipMemcpyHostToDevice, s));
-        DMX_HIP(hipMemcpyAsync(mix.f() + samples, right, samples * sizeof(float), hipMemcpyHostToDevice, s));
-        separate_device(nets, bag_weights, n_nets, stems_wanted, mix.f(), samples, sample_rate, o, progress, user,
-                        stems.f());
+        // Runs of consecutive wanted stems: one 2-D copy each.
+        std::vector<std::pair<int, int>> runs;
         for (int i = 0; i < S; ++i) {
             if (stems_wanted && !stems_wanted[i]) continue;
-            DMX_HIP(hipMemcpyAsync(stems_out + (int64_t)i * 2 * samples, stems.f() + (int64_t)i * 2 * samples,
-                                   2 * samples * sizeof(float), hipMemcpyDeviceToHost, s));
+            if (!runs.empty() && runs.back().first + runs.back().second == i)
+                ++runs.back().second;
+            else
+                runs.push_back({i, 1});
         }
-        DMX_HIP(hipStreamSynchronize(s));
+        const size_t row_bytes = (size_t)samples * sizeof(float);
+        const size_t need = (size_t)(2 + 2 * S) * row_bytes;
+        const bool staged = need <= pinned_limit();
+        DBuf mix = fbuf(s, 2 * samples), stems = fbuf(s, (int64_t)S * 2 * samples);
+        try {
+            float *pin_mix = nullptr, *pin_stems = nullptr;
+            if (staged) {
+                // Everything on the runner's main stream, in order: the mix
+                // goes up piece by piece (a piece's host copy overlaps the
+                // previous piece's DMA), and each group's finished samples
+                // come back into pinned memory as soon as they are final.
+                pin_mix = reinterpret_cast<float *>(r.staging.reserve(need));
+                pin_stems = pin_mix + 2 * samples;
+                const int64_t piece = 1 << 20;
+                const float *src[2] = {left, right};
+                for (int ch = 0; ch < 2; ++ch)
+                    for (int64_t off = 0; off < samples; off += piece) {
+                        const int64_t n = std::min(piece, samples - off);
+                        float *p = pin_mix + ch * samples + off;
+                        host_copy(p, src[ch] + off, (size_t)n * sizeof(float));
+                        DMX_HIP(hipMemcpyAsync(mix.f() + ch * samples + off, p, (size_t)n * sizeof(float),
+                                               hipMemcpyHostToDevice, s));
+                    }
+            } else {
+                r.ring.upload({{mix.f(), const_cast<float *>(left), row_bytes},
+                               {mix.f() + samples, const_cast<float *>(right), row_bytes}},
+                              s);
+            }
+            // Map the caller's output pages on the host threads while the GPU
+            // works (queued after the upload's copies; the pool runs jobs in
+            // order).
+            for (const auto &run : runs)
+                host_jobs.push_back(prefault_async(stems_out + (int64_t)run.first * 2 * samples,
+                                                   (size_t)run.second * 2 * row_bytes));
+            struct Block {
+                hipEvent_t ev;
+                int64_t lo, hi;
+            };
+            std::vector<Block> blocks;
+            // Readback blocks of about 4 MB over the wanted rows.
+            const int64_t wanted_rows = [&] {
+                int64_t n = 0;
+                for (const auto &run : runs) n += 2 * run.second;
+                return std::max<int64_t>(n, 1);
+            }();
+            const int64_t block = std::max<int64_t>(1 << 14, (int64_t)(4u << 20) / (wanted_rows * 4));
+            auto on_final = [&](int64_t lo, int64_t hi) {
+                for (int64_t a = lo; a < hi; a += block) {
+                    const int64_t b = std::min(hi, a + block);
+                    for (const auto &run : runs) {
+                        const int64_t at = (int64_t)run.first * 2 * samples + a;
+                        DMX_HIP(hipMemcpy2DAsync(pin_stems + at, row_bytes, stems.f() + at, row_bytes,
+                                                 (size_t)(b - a) * sizeof(float), (size_t)run.second * 2,
+                                                 hipMemcpyDeviceToHost, s));
+                    }
+                    Block bl{xfer_event(r, blocks.size()), a, b};
+                    DMX_HIP(hipEventRecord(bl.ev, s));
+                    blocks.push_back(bl);
+                }
+            };
+            std::vector<GroupMark> marks;
+            size_t total = 0;
+            if (staged)
+                separate_device(nets, bag_weights, n_nets, stems_wanted, mix.f(), samples, sample_rate, o, stems.f(),
+                                marks, total, on_final);
+            else
+                separate_device(nets, bag_weights, n_nets, stems_wanted, mix.f(), samples, sample_rate, o, stems.f(),
+                                marks, total);
+            size_t bi = 0;
+            for (const GroupMark &m : marks) {
+                for (; bi < blocks.size() && blocks[bi].hi <= m.hi; ++bi) {
+                    const Block &bl = blocks[bi];
+                    DMX_HIP(hipEventSynchronize(bl.ev));
+                    for (const auto &run : runs)
+                        for (int row = 2 * run.first; row < 2 * (run.first + run.second); ++row) {
+                            const int64_t at = (int64_t)row * samples + bl.lo;
+                            host_jobs.push_back(
+                                host_copy_async(stems_out + at, pin_stems + at, (size_t)(bl.hi - bl.lo) * sizeof(float)));
+                        }
+                }
+                if (progress) {
+                    DMX_HIP(hipEventSynchronize(m.ev));
+                    progress(m.done, total, user);
+                }
+            }
+            if (!staged) {
+                std::vector<Span> spans;
+                for (const auto &run : runs) {
+                    const int64_t at = (int64_t)run.first * 2 * samples;
+                    spans.push_back({stems.f() + at, stems_out + at, (size_t)run.second * 2 * row_bytes});
+                }
+                r.ring.download(spans, s);
+            }
+            DMX_HIP(hipStreamSynchronize(s));
+        } catch (...) {
+            // The device buffers go back to the pool: let nothing use them.
+            for (hipStream_t st : {r.stream, r.side, r.stream_b, r.side_b}) (void)hipStreamSynchronize(st);
+            throw;
+        }
     });
+    for (uint64_t t : host_jobs) HostPool::instance().wait(t);
+    return rc;
 }
 
 }  // extern "C"

@@ -101,18 +101,26 @@ int dmx_runner_create(const dmx_tensor *weights, size_t n_weights, const dmx_con
 void dmx_runner_destroy(dmx_runner *runner);
 /* "hip:<device name>" (describe / backend_tag, api.rs:1038-1045, 821). */
 const char *dmx_runner_backend_tag(const dmx_runner *runner);
-/* The runner's hipStream_t, for callers that order their own device work after it. */
+/* The runner's main hipStream_t, for callers that order their own device work
+ * after it: the device entry points finish their work on it (a group queued by
+ * dmx_forward_start may run on the runner's second stream pair; dmx_synchronize
+ * waits for every stream). */
 void *dmx_runner_stream(dmx_runner *runner);
 int dmx_synchronize(dmx_runner *runner);
 
 /* SegmentForward::start (crates/demucs-core/src/demucs/pipeline.rs:178-190):
  * queues a forward of `mix` (batch, channels, length), length <= training_length,
  * and returns with the work in flight. The host array may be reused on return.
- * Two groups may be in flight; a pending group's buffers are never reused. */
+ * Groups in flight are not limited (the caller of the reference keeps two);
+ * each holds a pinned staging slot of the runner until it is collected, and
+ * consecutive groups run on alternating stream pairs so they overlap. Slots
+ * are reused, so steady state allocates nothing. */
 int dmx_forward_start(dmx_runner *runner, const float *mix, int64_t batch, int64_t channels,
                       int64_t length, dmx_pending **out);
 /* SegmentForward::collect: waits for that group only and writes
- * (batch, sources, channels, length) into `stems`; frees `pending`. */
+ * (batch, sources, channels, length) into `stems`; frees `pending`.
+ * A null argument or a group of another runner is an error that leaves the
+ * group pending; groups may be collected in any order. */
 int dmx_forward_collect(dmx_runner *runner, dmx_pending *pending, float *stems);
 /* Htdemucs::forward (crates/demucs-core/src/demucs/host.rs:202-520), synchronous. */
 int dmx_forward(dmx_runner *runner, const float *mix, int64_t batch, int64_t channels,
@@ -157,12 +165,19 @@ typedef void (*dmx_progress_fn)(size_t done, size_t total, void *user);
  *  nets[n_nets], bag_weights (n_nets x sources, row-major; NULL = identity-free
  *  single network), stems_wanted[sources] (NULL = all).
  *  left/right: host samples; stems_out: (sources, 2, samples) host, rows of
- *  unwanted stems are left untouched. */
+ *  unwanted stems are left untouched.
+ * The mix goes up through the runner's pinned staging; each chunk group's
+ * finished output samples are read back while later groups compute, the
+ * reference's OlaRing flush after each segment (streaming.rs:96-261,
+ * :389-394). `progress(done, total, user)` runs on the calling thread after
+ * each group; it does not change the schedule on the GPU. */
 int dmx_separate(dmx_runner *const *nets, const float *bag_weights, int32_t n_nets,
                  const uint8_t *stems_wanted, const float *left, const float *right,
                  int64_t samples, int32_t sample_rate, const dmx_separate_options *opts,
                  dmx_progress_fn progress, void *user, float *stems_out);
-/* Same with device-resident mix (2, samples) and stems (sources, 2, samples). */
+/* Same with device-resident mix (2, samples) and stems (sources, 2, samples),
+ * enqueued on the runner's stream; without a progress callback it returns
+ * before the GPU has finished. */
 int dmx_separate_device(dmx_runner *const *nets, const float *bag_weights, int32_t n_nets,
                         const uint8_t *stems_wanted, const float *d_mix, int64_t samples,
                         int32_t sample_rate, const dmx_separate_options *opts,

@@ -127,15 +127,20 @@ def test_separation_matches_oracle(dmx, oracle, small, shifts, group, progress):
 
 @pytest.mark.parametrize("group", [1, 2])
 def test_two_lane_schedule_matches_one_lane(dmx, small, group):
-    """The same separation with one stream pair (a progress callback makes
-    the host wait per group) and with alternating pairs, the second pair's
-    group starting when the first reaches its transformer: the stems agree to
-    the f64 atomics' summation order (far tighter than the 60 dB parity
-    gate), so no buffer is reused or read across the lanes too early."""
+    """The same separation with one stream pair (a trace sink that records
+    nothing keeps the whole run on the main stream) and with alternating
+    pairs, the second pair's group starting when the first reaches its
+    transformer: the stems agree to the f64 atomics' summation order (far
+    tighter than the 60 dB parity gate), so no buffer is reused or read
+    across the lanes too early."""
     cfg, weights, runner, model = small
     mix = dmx.signals.synthetic_mix(13, 1.6)
     opts = dmx.SeparateOptions(shifts=0, overlap=0.25, batch_chunks=group)
-    one = dmx.separate_runners([runner], mix[0], mix[1], 44100, opts, on_progress=lambda p: None)
+    runner.set_trace(lambda name: False, lambda name, a: None)
+    try:
+        one = dmx.separate_runners([runner], mix[0], mix[1], 44100, opts)
+    finally:
+        runner.set_trace(None, None)
     two = dmx.separate_runners([runner], mix[0], mix[1], 44100, opts)
     for s in range(4):
         assert snr_db(one[s], two[s]) >= 120.0, (s, snr_db(one[s], two[s]))
