@@ -78,6 +78,7 @@ SIGNATURES = {
     "dmx_op_gelu": (_I, [_VP, _VP, _I64, _VP]),
     "dmx_op_set_precision": (_I, [_I]),
     "dmx_op_spec_normalise": (_I, [_VP, _VP, _I, _I, _VP, _VP, _VP]),
+    "dmx_op_spec_normalise_noalloc": (_I, [_VP, _VP, _I, _I, _VP, _VP, _VP]),
     "dmx_op_ispec_sum": (_I, [_VP, _VP, _VP, _I, _I, _VP, _VP]),
     # include/dmx_ckpt.h
     "dmx_checkpoint_load": (_I, [ctypes.c_char_p, ctypes.POINTER(_VP)]),

@@ -2,7 +2,9 @@
 // caller's stream, for the parity tests.
 #include <hip/hip_runtime.h>
 
+#include <map>
 #include <memory>
+#include <mutex>
 #include <vector>
 
 #include "../../include/dmx_ops.h"
@@ -48,6 +50,48 @@ const float *gemm_weights(hipStream_t s, const float *w, int oc, int ic, int kh,
     keep = std::make_unique<Scratch>(n * sizeof(float));
     DMX_HIP(hipMemcpy(keep->p, g.data(), n * sizeof(float), hipMemcpyHostToDevice));
     return static_cast<const float *>(keep->p);
+}
+
+// ---- fixed scratch of dmx_op_spec_normalise_noalloc ----
+// Layout: the 4096-point twiddles and periodic Hann window (8192 floats),
+// then the f64 moments (4 per batch row), then the STFT frames
+// (batch x frames x 2 channels x 2048 bins x complex).
+constexpr int NOALLOC_MAX_BATCH = 64;
+constexpr int64_t NOALLOC_MAX_FRAMES = 672;  // batch x ceil(L / 1024): two 7.8 s segments
+constexpr size_t NOALLOC_TW_BYTES = (size_t)(4096 + 4096) * sizeof(float);
+constexpr size_t NOALLOC_STATS_BYTES = (size_t)4 * NOALLOC_MAX_BATCH * sizeof(double);
+constexpr size_t NOALLOC_FRAME_FLOATS = (size_t)2 * 2048 * 2;
+constexpr size_t NOALLOC_BYTES =
+    NOALLOC_TW_BYTES + NOALLOC_STATS_BYTES + (size_t)NOALLOC_MAX_FRAMES * NOALLOC_FRAME_FLOATS * sizeof(float);
+static_assert(NOALLOC_TW_BYTES % 256 == 0 && NOALLOC_STATS_BYTES % 256 == 0, "scratch sections stay 256-B aligned");
+
+}  // namespace
+
+// Each GPU holds its own copy (about 22 MB) from the library's load until the
+// process ends. Host code never uses this name as an address: the per-device
+// address comes from hipGetSymbolAddress (scratch_on_current_device).
+static __device__ __align__(256) unsigned char scratch[NOALLOC_BYTES];
+
+namespace {
+
+// The current device's address of `scratch`; the first call on a device also
+// writes the twiddle table into it (a synchronous copy, no allocation).
+unsigned char *scratch_on_current_device() {
+    static std::mutex mu;
+    static std::map<int, unsigned char *> ptrs;
+    int dev = -1;
+    DMX_HIP(hipGetDevice(&dev));
+    std::lock_guard<std::mutex> lock(mu);
+    auto it = ptrs.find(dev);
+    if (it != ptrs.end()) return it->second;
+    void *p = nullptr;
+    DMX_HIP(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+    if (!p) throw Error(6, "hipGetSymbolAddress returned no address for the fixed scratch");
+    std::vector<float> tw(NOALLOC_TW_BYTES / sizeof(float));
+    make_twiddles(4096, tw.data());
+    DMX_HIP(hipMemcpy(p, tw.data(), NOALLOC_TW_BYTES, hipMemcpyHostToDevice));
+    ptrs[dev] = static_cast<unsigned char *>(p);
+    return ptrs[dev];
 }
 
 }  // namespace
@@ -231,6 +275,25 @@ int dmx_op_spec_normalise(void *stream, const float *mix, int b, int L, float *x
         spec_and_normalise(s, mix, b, L, 4096, static_cast<float *>(frames.p), xspec, xwave, norms,
                            static_cast<double *>(st.p), twiddles_4096());
         DMX_HIP(hipStreamSynchronize(s));
+    });
+}
+
+int dmx_op_spec_normalise_noalloc(void *stream, const float *mix, int b, int L, float *xspec, float *xwave,
+                                  float *norms) {
+    return guarded([&] {
+        hipStream_t s = as_stream(stream);
+        if (b <= 0 || L <= 0) throw Error(1, "dmx_op_spec_normalise_noalloc: empty input");
+        const int64_t frames = (int64_t)b * ceil_div(L, 1024);
+        if (b > NOALLOC_MAX_BATCH || frames > NOALLOC_MAX_FRAMES)
+            throw Error(1, "dmx_op_spec_normalise_noalloc: batch " + std::to_string(b) + " x " +
+                               std::to_string(ceil_div(L, 1024)) + " frames exceeds the fixed scratch (at most " +
+                               std::to_string(NOALLOC_MAX_BATCH) + " rows and " + std::to_string(NOALLOC_MAX_FRAMES) +
+                               " batch frames, two 7.8 s segments); use dmx_op_spec_normalise");
+        unsigned char *base = scratch_on_current_device();
+        const float *twiddles = reinterpret_cast<const float *>(base);
+        double *stats = reinterpret_cast<double *>(base + NOALLOC_TW_BYTES);
+        float *frame_buf = reinterpret_cast<float *>(base + NOALLOC_TW_BYTES + NOALLOC_STATS_BYTES);
+        spec_and_normalise(s, mix, b, L, 4096, frame_buf, xspec, xwave, norms, stats, twiddles);
     });
 }
 

@@ -80,6 +80,17 @@ int dmx_op_gelu(void *stream, const float *x, int64_t n, float *out);
 /* stft_cac_into + batch_moments + batch_normalize (kernels.rs:3662-3870):
  * mix (b, 2, L) -> xspec (b, 4, 2048, le), xwave (b, 2, L), norms (b, 4) = (mean, std, mean_t, std_t). */
 int dmx_op_spec_normalise(void *stream, const float *mix, int b, int L, float *xspec, float *xwave, float *norms);
+/* dmx_op_spec_normalise without allocating: no counterpart in the reference.
+ * For callers that cannot call hipMalloc (code under HIP graph capture,
+ * serving loops, harnesses that forbid it). The STFT frames and moments live
+ * in the library's fixed device scratch (about 22 MB per GPU, held until the
+ * process ends): at most 64 batch rows and b * ceil(L / 1024) <= 672 (two
+ * 7.8 s segments); larger inputs are a DMX_ERR_SHAPE error. Asynchronous on
+ * `stream`. The first call on a device sets the scratch up (a synchronous
+ * 32 KB table copy): make it before capturing. Calls on one GPU share its
+ * scratch, so calls that overlap on one GPU race. */
+int dmx_op_spec_normalise_noalloc(void *stream, const float *mix, int b, int L, float *xspec, float *xwave,
+                                  float *norms);
 /* ispec_cac_into + final sum (kernels.rs:3877-3973): xspec (b, 16, 2048, le), xtime (b, 8, L),
  * norms (b, 4) -> stems (b, 4, 2, L). */
 int dmx_op_ispec_sum(void *stream, const float *xspec, const float *xtime, int b, int L, const float *norms,
