@@ -86,3 +86,48 @@ def test_a_bag_is_the_weight_normalised_sum_of_its_networks(dmx, oracle):
         assert snr_db(expect, both[s]) > 100.0, s
     np.testing.assert_array_equal(both[0], single[0][0])
     np.testing.assert_array_equal(both[2], single[1][2])
+
+
+def _triangle(seg, power):
+    """The weight of crates/demucs-core/src/demucs/pipeline.rs:117-131 written
+    out here: 1..=seg/2 rising, then seg - seg/2 down to 1, divided by its
+    maximum, raised to `power`."""
+    half = seg // 2
+    w = np.concatenate([np.arange(1, half + 1), np.arange(seg - half, 0, -1)]).astype(np.float64)
+    return (w / max(w.max(), 1.0)) ** power
+
+
+@pytest.mark.parametrize("length,seg,power,group", [(1000, 160, 1.0, 1), (1000, 161, 1.0, 2), (777, 100, 2.0, 3),
+                                                    (5000, 1000, 0.5, 4)])
+def test_overlap_add_weights_chunks_by_the_triangle(oracle, length, seg, power, group):
+    """A stand-in forward that answers chunk i with the constant i + 1: the
+    overlap-add at sample t must be sum_i w(t - s_i) (i + 1) / sum_i w(t - s_i)
+    over the chunks covering t (splice_group, pipeline.rs:660-699: a chunk of
+    length n uses weights [0, n) and the centre-trimmed output). A wrong
+    weight shape, offset or normalisation changes the ratio."""
+    calls = []
+
+    def index_forward(chunk):
+        first = sum(calls)  # chunks answered by earlier groups
+        calls.append(chunk.shape[0])
+        out = np.empty((chunk.shape[0], 4) + chunk.shape[1:], np.float32)
+        for j in range(chunk.shape[0]):
+            out[j] = first + j + 1
+        return out
+
+    mix = np.zeros((1, 2, length), np.float32)
+    out = oracle.split_pass(mix, seg, 0.25, power, 0, 0, group, 4, index_forward)
+    stride = int(0.75 * seg)
+    starts = list(range(0, length, stride))
+    assert sum(calls) == len(starts)
+    w = _triangle(seg, power)
+    num = np.zeros(length)
+    den = np.zeros(length)
+    for i, s0 in enumerate(starts):
+        n = min(length - s0, seg)
+        num[s0:s0 + n] += w[:n] * (i + 1)
+        den[s0:s0 + n] += w[:n]
+    expect = num / den
+    for s in range(4):
+        for c in range(2):
+            np.testing.assert_allclose(out[0, s, c], expect, rtol=2e-6)
