@@ -1,26 +1,28 @@
 // checkpoint.hip — host-side checkpoint readers behind include/dmx_ckpt.h
 // (no device code).
 //
-// Two containers, as `load_weights` (crates/demucs-core/src/demucs/weights.rs:30-88)
-// accepts them:
-//   * safetensors (crates/demucs-core/src/safetensors.rs:38-139): u64 LE header
-//     length, a JSON header {name: {dtype, shape, data_offsets}, "__metadata__":
-//     {str: str}}, then the data; tensors of any listed dtype become f32, and the
+// Two containers, the ones `load_weights` accepts
+// (crates/demucs-core/src/demucs/weights.rs:30-88); the readers are this
+// build's own and share only the file formats with the reference's
+// (crates/demucs-core/src/safetensors.rs, crates/demucs-core/src/ckpt/):
+//   * safetensors: tensors of any listed element type become f32, and the
 //     model config comes from the "kwargs" metadata entry when present
 //     (HtdemucsConfig::from_kwargs_json, config.rs:150-215);
-//   * torch.save zips (crates/demucs-core/src/ckpt/mod.rs:43-120): "<root>/data.pkl"
-//     (a pickle), "<root>/data/<key>" (one raw blob per storage) and
-//     "<root>/byteorder". The pickle is read by a data-only interpreter
-//     (ckpt/pickle.rs:140-460 models the same opcodes): it builds lists, dicts and
-//     tuples, and recognises torch's tensor-rebuild and OrderedDict reductions by
-//     name; every other reduction becomes an opaque value. Nothing named in the
-//     file is imported or called. The state dict is the top-level dict or its
-//     "model_state_dict" / "state_dict" / "state" entry (mod.rs:232-256).
+//   * torch.save zips: "<root>/data.pkl" (a pickle), "<root>/data/<key>" (one
+//     raw blob per storage) and "<root>/byteorder". The pickle is evaluated
+//     symbolically (PickleMachine): calls are recorded, never made, and the
+//     tensors are recognised in the finished tree by their rebuild calls.
+//     The state dict is the top-level dict or its "model_state_dict" /
+//     "state_dict" / "state" entry, the keys demucs' packages and training
+//     checkpoints use (crates/demucs-core/src/ckpt/mod.rs:232-256).
 // Tensors are kept sorted by name, each contiguous row-major f32.
 #include <algorithm>
+#include <array>
 #include <cctype>
 #include <cerrno>
 #include <cmath>
+#include <cstdio>
+#include <cstdlib>
 #include <cstring>
 #include <limits>
 #include <fstream>
@@ -322,40 +324,6 @@ void decode(const uint8_t *p, size_t n, DType t, bool big, float *out) {
     }
 }
 
-bool safetensors_dtype(const std::string &s, DType &t) {
-    static const std::pair<const char *, DType> table[] = {
-        {"F32", DType::F32}, {"F64", DType::F64}, {"F16", DType::F16}, {"BF16", DType::BF16},
-        {"I64", DType::I64}, {"I32", DType::I32}, {"I16", DType::I16}, {"I8", DType::I8},
-        {"U8", DType::U8},   {"BOOL", DType::Bool}};
-    for (const auto &e : table)
-        if (s == e.first) {
-            t = e.second;
-            return true;
-        }
-    return false;
-}
-
-// Storage class ("HalfStorage") or dtype ("torch.float16", "float16") spellings.
-bool torch_dtype(std::string s, DType &t) {
-    std::transform(s.begin(), s.end(), s.begin(), [](unsigned char c) { return (char)std::tolower(c); });
-    if (s.rfind("torch.", 0) == 0) s = s.substr(6);
-    static const std::pair<const char *, DType> table[] = {
-        {"floatstorage", DType::F32},  {"float", DType::F32},    {"float32", DType::F32},
-        {"halfstorage", DType::F16},   {"half", DType::F16},     {"float16", DType::F16},
-        {"bfloat16storage", DType::BF16}, {"bfloat16", DType::BF16},
-        {"doublestorage", DType::F64}, {"double", DType::F64},   {"float64", DType::F64},
-        {"bytestorage", DType::U8},    {"uint8", DType::U8},     {"charstorage", DType::I8},
-        {"int8", DType::I8},           {"shortstorage", DType::I16}, {"int16", DType::I16},
-        {"intstorage", DType::I32},    {"int32", DType::I32},    {"longstorage", DType::I64},
-        {"int64", DType::I64},         {"boolstorage", DType::Bool}, {"bool", DType::Bool}};
-    for (const auto &e : table)
-        if (s == e.first) {
-            t = e.second;
-            return true;
-        }
-    return false;
-}
-
 // ----- the checkpoint object -----
 
 struct Tensor {
@@ -459,52 +427,102 @@ void config_from_kwargs(const Json &kw, dmx_config &cfg) {
 }
 
 // ----- safetensors -----
+// An 8-byte little-endian header size h, then h bytes of JSON that map each
+// tensor name to {"dtype", "shape", "data_offsets": [begin, end)} (offsets
+// into the data section after the header), plus an optional "__metadata__"
+// object of strings. Every entry is checked before any tensor is decoded.
+
+struct StEntry {
+    std::string name;
+    DType type;
+    std::vector<int64_t> shape;
+    uint64_t begin = 0, end = 0;
+};
+
+// Element types by their safetensors spelling (all widen to f32).
+const std::map<std::string, DType> &st_types() {
+    static const std::map<std::string, DType> types = {
+        {"BOOL", DType::Bool}, {"U8", DType::U8},   {"I8", DType::I8},   {"I16", DType::I16}, {"I32", DType::I32},
+        {"I64", DType::I64},   {"F16", DType::F16}, {"BF16", DType::BF16}, {"F32", DType::F32}, {"F64", DType::F64}};
+    return types;
+}
+
+[[noreturn]] void st_fail(const std::string &tensor, const std::string &what) {
+    bad("safetensors tensor `" + tensor + "`: " + what);
+}
+
+// A list of non-negative integers under `key` of a header entry.
+std::vector<int64_t> st_ints(const Json &entry, const char *key, const std::string &tensor) {
+    const Json *v = entry.get(key);
+    if (!v || v->kind != Json::Array) st_fail(tensor, std::string("its header entry lacks a `") + key + "` list");
+    std::vector<int64_t> out;
+    for (const Json &x : v->items) {
+        if (x.kind != Json::Number || !x.integral || x.inum < 0)
+            st_fail(tensor, std::string("`") + key + "` holds a value that is not a non-negative integer");
+        out.push_back(x.inum);
+    }
+    return out;
+}
+
+std::string shape_text(const std::vector<int64_t> &shape) {
+    std::string s = "[";
+    for (size_t i = 0; i < shape.size(); ++i) s += (i ? ", " : "") + std::to_string(shape[i]);
+    return s + "]";
+}
+
+StEntry st_entry(const std::string &name, const Json &e, uint64_t data_bytes) {
+    if (e.kind != Json::Object) st_fail(name, "its header entry is not an object");
+    StEntry t;
+    t.name = name;
+    const Json *dt = e.get("dtype");
+    if (!dt || dt->kind != Json::String) st_fail(name, "its header entry lacks a `dtype` string");
+    const auto ty = st_types().find(dt->str);
+    if (ty == st_types().end()) st_fail(name, "element type `" + dt->str + "` is not one this reader widens to f32");
+    t.type = ty->second;
+    t.shape = st_ints(e, "shape", name);
+    const std::vector<int64_t> span = st_ints(e, "data_offsets", name);
+    if (span.size() != 2) st_fail(name, "`data_offsets` must be the pair [begin, end]");
+    t.begin = (uint64_t)span[0];
+    t.end = (uint64_t)span[1];
+    if (t.begin > t.end || t.end > data_bytes)
+        st_fail(name, "its bytes [" + std::to_string(t.begin) + ", " + std::to_string(t.end) + ") lie beyond the " +
+                          std::to_string(data_bytes) + "-byte data section");
+    const uint64_t need = checked_product(t.shape, name) * (uint64_t)dtype_size(t.type);
+    if (t.end - t.begin != need)
+        st_fail(name, "shape " + shape_text(t.shape) + " of " + dt->str + " takes " + std::to_string(need) +
+                          " bytes, but its entry spans " + std::to_string(t.end - t.begin));
+    return t;
+}
 
 void parse_safetensors(const uint8_t *bytes, size_t len, dmx_checkpoint &c) {
-    if (len < 8) bad("safetensors file is shorter than its header length");
-    uint64_t hlen;
-    std::memcpy(&hlen, bytes, 8);  // little-endian host
-    if (hlen > len - 8)
-        bad("safetensors header claims " + std::to_string(hlen) + " bytes but the file holds " + std::to_string(len));
-    const Json header = parse_json(reinterpret_cast<const char *>(bytes) + 8, (size_t)hlen);
-    if (header.kind != Json::Object) bad("safetensors header is not an object");
-    const uint8_t *data = bytes + 8 + hlen;
-    const uint64_t data_len = len - 8 - hlen;
+    if (len < 8)
+        bad("safetensors: " + std::to_string(len) + " bytes cannot hold the 8-byte header size that starts the file");
+    const uint64_t header_bytes = load_as<uint64_t>(bytes, false);
+    if (header_bytes > len - 8)
+        bad("safetensors: the header size field announces " + std::to_string(header_bytes) + " bytes, but only " +
+            std::to_string(len - 8) + " follow it");
+    const Json header = parse_json(reinterpret_cast<const char *>(bytes) + 8, (size_t)header_bytes);
+    if (header.kind != Json::Object) bad("safetensors: the header is not a JSON object");
+    const uint8_t *data = bytes + 8 + header_bytes;
+    const uint64_t data_bytes = len - 8 - header_bytes;
+    std::vector<StEntry> entries;
     for (const auto &m : header.members) {
-        const std::string &name = m.first;
-        const Json &e = m.second;
-        if (name == "__metadata__") {
-            for (const auto &kv : e.members)
+        if (m.first == "__metadata__") {
+            if (m.second.kind != Json::Object) bad("safetensors: `__metadata__` is not an object");
+            for (const auto &kv : m.second.members)
                 if (kv.second.kind == Json::String) c.metadata[kv.first] = kv.second.str;
             continue;
         }
-        const Json *dt = e.get("dtype"), *sh = e.get("shape"), *off = e.get("data_offsets");
-        if (!dt || dt->kind != Json::String) bad(name + ": no dtype");
-        if (!sh || sh->kind != Json::Array) bad(name + ": no shape");
-        if (!off || off->kind != Json::Array) bad(name + ": no data_offsets");
-        if (off->items.size() != 2) bad(name + ": malformed data_offsets");
-        DType t;
-        if (!safetensors_dtype(dt->str, t)) bad(name + ": unsupported safetensors dtype " + dt->str);
-        Tensor tensor;
-        for (const Json &d : sh->items) {
-            if (d.kind != Json::Number || !d.integral || d.inum < 0) bad(name + ": bad shape entry");
-            tensor.shape.push_back(d.inum);
-        }
-        for (const Json &o : off->items)
-            if (o.kind != Json::Number || !o.integral || o.inum < 0) bad(name + ": bad data offset");
-        const uint64_t begin = (uint64_t)off->items[0].inum, stop = (uint64_t)off->items[1].inum;
-        if (stop < begin || stop > data_len)
-            bad(name + ": data range [" + std::to_string(begin) + ", " + std::to_string(stop) + ") is outside the " +
-                std::to_string(data_len) + " data bytes");
-        const uint64_t n = checked_product(tensor.shape, name);
-        if (stop - begin != n * (uint64_t)dtype_size(t))
-            bad(name + ": " + std::to_string(stop - begin) + " data bytes do not match " + std::to_string(n) +
-                " elements of " + dt->str);
-        tensor.data.resize(n);
-        decode(data + begin, n, t, false, tensor.data.data());
-        c.tensors[name] = std::move(tensor);
+        entries.push_back(st_entry(m.first, m.second, data_bytes));
     }
-    auto kw = c.metadata.find("kwargs");
+    for (const StEntry &e : entries) {
+        Tensor t;
+        t.shape = e.shape;
+        t.data.resize((e.end - e.begin) / (uint64_t)dtype_size(e.type));
+        decode(data + e.begin, t.data.size(), e.type, false, t.data.data());
+        if (!c.tensors.emplace(e.name, std::move(t)).second) bad("safetensors: tensor `" + e.name + "` is listed twice");
+    }
+    const auto kw = c.metadata.find("kwargs");
     if (kw != c.metadata.end()) config_from_kwargs(parse_json(kw->second.data(), kw->second.size()), c.config);
 }
 
@@ -581,452 +599,590 @@ std::pair<const uint8_t *, uint64_t> zip_data(const uint8_t *z, size_t len, cons
     return {z + start, e.size};
 }
 
-// ----- the pickle interpreter -----
+// ----- pickles, evaluated symbolically -----
+// torch.save stores the state dict as a pickle: a small stack program whose
+// objects are made by calling importable functions
+// (torch._utils._rebuild_tensor_v2, collections.OrderedDict, ...) and whose
+// storages are named by "persistent ids" that point at archive entries. This
+// reader runs the stack program without importing or calling anything: a
+// call leaves an `Apply` node holding the callee's dotted name and its
+// arguments, a persistent id leaves a `Persistent` node, and the tensors are
+// recognised afterwards by walking the finished tree (torch_tensor below).
+// Opcode numbers and meanings are those of the pickle format (CPython's
+// Lib/pickle.py and pickletools); torch writes protocol 2.
 
-struct PVal;
-using PRef = std::shared_ptr<PVal>;
+struct PNode;
+using PNodeRef = std::shared_ptr<PNode>;
 
-struct StorageRef {
-    DType dtype = DType::F32;
-    std::string key;
-    int64_t numel = 0;
+struct PNode {
+    enum class Shape : uint8_t { Nil, Truth, Whole, Real, Text, Raw, Row, Table, Name, Apply, Persistent };
+    Shape shape = Shape::Nil;
+    bool tuple = false;                                // Row: a tuple rather than a list
+    int64_t whole = 0;                                 // Truth (0 or 1), Whole
+    double real = 0.0;                                 // Real
+    std::string text;                                  // Text, Raw; Name: "module.qualname"
+    std::vector<PNodeRef> row;                         // Row items; Apply, Persistent: the arguments
+    std::vector<std::pair<PNodeRef, PNodeRef>> table;  // Table entries; Apply: items stored into the result
+    PNodeRef callee, state;                            // Apply: the Name called, and the state BUILD gave it
 };
-struct TensorRef {
-    StorageRef storage;
-    int64_t offset = 0;
-    bool dense = false;  // false: a sparse layout (not supported)
-    std::vector<int64_t> size, stride;
-};
 
-struct PVal {
-    enum Kind { None, Bool, Int, Float, Str, Bytes, Tuple, List, Dict, Global, Storage, Tensor, Opaque } kind = None;
-    int64_t i = 0;
-    double f = 0.0;
-    std::string s, s2;  // Str / Bytes / Opaque: s; Global: module s, name s2
-    std::vector<PRef> items;
-    std::vector<std::pair<PRef, PRef>> dict;
-    StorageRef storage;
-    TensorRef tensor;
-};
-
-PRef mk(PVal::Kind k) {
-    auto v = std::make_shared<PVal>();
-    v->kind = k;
-    return v;
+PNodeRef node(PNode::Shape shape) {
+    auto n = std::make_shared<PNode>();
+    n->shape = shape;
+    return n;
 }
 
-class Unpickler {
+class PickleMachine {
   public:
-    Unpickler(const uint8_t *p, size_t n) : p_(p), end_(p + n) {}
+    PickleMachine(const uint8_t *p, size_t n) : begin_(p), at_(p), end_(p + n) {}
 
-    PRef run() {
-        while (true) {
-            const uint8_t op = u8();
-            switch (op) {
-                case 0x80: u8(); break;                     // PROTO
-                case '.': return pop();                     // STOP
-                case 0x95: take(8); break;                  // FRAME
-                case '(': marks_.push_back(stack_.size()); break;  // MARK
-                case ')': push(mk(PVal::Tuple)); break;    // EMPTY_TUPLE
-                case ']': push(mk(PVal::List)); break;     // EMPTY_LIST
-                case '}': push(mk(PVal::Dict)); break;     // EMPTY_DICT
-                case 'N': push(mk(PVal::None)); break;     // NONE
-                case 0x88: push_bool(true); break;         // NEWTRUE
-                case 0x89: push_bool(false); break;        // NEWFALSE
-                case 'K': push_int(u8()); break;           // BININT1
-                case 'M': push_int(rd16(take(2))); break;  // BININT2
-                case 'J': push_int((int32_t)rd32(take(4))); break;  // BININT
-                case 'I': {                                // INT (text)
-                    std::string t = line();
-                    while (!t.empty() && (t.back() == 'L' || t.back() == ' ')) t.pop_back();
-                    if (t == "01") push_bool(true);
-                    else if (t == "00") push_bool(false);
-                    else push_int(parse_int(t));
-                    break;
-                }
-                case 0x8a: push_int(long_le(take(u8()), 0)); break;  // LONG1
-                case 0x8b: {                                          // LONG4
-                    const uint32_t n = rd32(take(4));
-                    push_int(long_le(take(n), n));
-                    break;
-                }
-                case 'F': {  // FLOAT (text)
-                    auto v = mk(PVal::Float);
-                    v->f = std::strtod(line().c_str(), nullptr);
-                    push(v);
-                    break;
-                }
-                case 'G': {  // BINFLOAT, big-endian
-                    auto v = mk(PVal::Float);
-                    v->f = load_as<double>(take(8), true);
-                    push(v);
-                    break;
-                }
-                case 'X': push_str(PVal::Str, rd32(take(4))); break;      // BINUNICODE
-                case 0x8c: push_str(PVal::Str, u8()); break;             // SHORT_BINUNICODE
-                case 0x8d: push_str(PVal::Str, rd64(take(8))); break;    // BINUNICODE8
-                case 'C': push_str(PVal::Bytes, u8()); break;            // SHORT_BINBYTES
-                case 'B': push_str(PVal::Bytes, rd32(take(4))); break;   // BINBYTES
-                case 0x8e: push_str(PVal::Bytes, rd64(take(8))); break;  // BINBYTES8
-                case 't': {  // TUPLE
-                    auto v = mk(PVal::Tuple);
-                    v->items = pop_mark();
-                    push(v);
-                    break;
-                }
-                case 0x85: case 0x86: case 0x87: {  // TUPLE1..3
-                    const int n = op - 0x84;
-                    auto v = mk(PVal::Tuple);
-                    if (stack_.size() < (size_t)n) fail("stack underflow");
-                    v->items.assign(stack_.end() - n, stack_.end());
-                    stack_.resize(stack_.size() - n);
-                    push(v);
-                    break;
-                }
-                case 'l': {  // LIST
-                    auto v = mk(PVal::List);
-                    v->items = pop_mark();
-                    push(v);
-                    break;
-                }
-                case 'a': {  // APPEND
-                    PRef item = pop();
-                    top(PVal::List, "APPEND")->items.push_back(item);
-                    break;
-                }
-                case 'e': {  // APPENDS
-                    auto items = pop_mark();
-                    auto &dst = top(PVal::List, "APPENDS")->items;
-                    dst.insert(dst.end(), items.begin(), items.end());
-                    break;
-                }
-                case 'd': {  // DICT
-                    auto v = mk(PVal::Dict);
-                    v->dict = pairs(pop_mark());
-                    push(v);
-                    break;
-                }
-                case 's': {  // SETITEM
-                    PRef val = pop(), key = pop();
-                    top(PVal::Dict, "SETITEM")->dict.emplace_back(key, val);
-                    break;
-                }
-                case 'u': {  // SETITEMS
-                    auto kv = pairs(pop_mark());
-                    auto &dst = top(PVal::Dict, "SETITEMS")->dict;
-                    dst.insert(dst.end(), kv.begin(), kv.end());
-                    break;
-                }
-                case 'c': {  // GLOBAL: a name only, never resolved
-                    auto v = mk(PVal::Global);
-                    v->s = line();
-                    v->s2 = line();
-                    push(v);
-                    break;
-                }
-                case 0x93: {  // STACK_GLOBAL
-                    PRef name = pop(), module = pop();
-                    auto v = mk(PVal::Global);
-                    v->s = text(module);
-                    v->s2 = text(name);
-                    push(v);
-                    break;
-                }
-                case 'q': memoize(u8()); break;          // BINPUT
-                case 'r': memoize(rd32(take(4))); break;  // LONG_BINPUT
-                case 0x94: memoize(memo_.size()); break;  // MEMOIZE
-                case 'p': memoize((uint64_t)parse_int(line())); break;  // PUT
-                case 'h': push(recall(u8())); break;                  // BINGET
-                case 'j': push(recall(rd32(take(4)))); break;         // LONG_BINGET
-                case 'g': push(recall((uint64_t)parse_int(line()))); break;  // GET
-                case 'Q': push(persistent(pop())); break;             // BINPERSID
-                case 'P': {                                           // PERSID (text)
-                    auto v = mk(PVal::Opaque);
-                    v->s = "PERSID(" + line() + ")";
-                    push(v);
-                    break;
-                }
-                case 'R': {  // REDUCE
-                    PRef args = pop(), fn = pop();
-                    push(reduce(fn, args));
-                    break;
-                }
-                case 0x81: {  // NEWOBJ
-                    PRef args = pop(), cls = pop();
-                    push(reduce(cls, args));
-                    break;
-                }
-                case 0x92: {  // NEWOBJ_EX
-                    pop();
-                    PRef args = pop(), cls = pop();
-                    push(reduce(cls, args));
-                    break;
-                }
-                case 'b': pop(); break;  // BUILD: object state (OrderedDict metadata, ...) is not needed
-                case '0': pop(); break;  // POP
-                case '1': pop_mark(); break;  // POP_MARK
-                case '2': push(top_any()); break;  // DUP
-                default: {
-                    char buf[64];
-                    std::snprintf(buf, sizeof buf, "unsupported pickle opcode 0x%02x at offset %zu", op,
-                                  (size_t)(p_ - start_) - 1);
-                    bad(buf);
-                }
+    PNodeRef evaluate() {
+        while (!result_) {
+            op_at_ = (size_t)(at_ - begin_);
+            if (at_ == end_) fail("the data ends before a STOP opcode");
+            const uint8_t op = byte();
+            const Step step = steps()[op];
+            if (!step) {
+                char hex[8];
+                std::snprintf(hex, sizeof hex, "0x%02x", op);
+                fail(std::string("opcode ") + hex + " is not one this reader runs");
             }
+            (this->*step)(op);
         }
+        return result_;
     }
 
   private:
-    const uint8_t *p_, *end_, *start_ = p_;
-    std::vector<PRef> stack_;
-    std::vector<size_t> marks_;
-    std::map<uint64_t, PRef> memo_;
+    using Step = void (PickleMachine::*)(uint8_t);
 
-    [[noreturn]] void fail(const std::string &m) { bad("pickle: " + m); }
-    const uint8_t *take(uint64_t n) {
-        if (n > (uint64_t)(end_ - p_)) fail("truncated stream");
-        const uint8_t *q = p_;
-        p_ += n;
-        return q;
+    // One handler per opcode byte; bytes without one are refused.
+    static const std::array<Step, 256> &steps() {
+        static const std::array<Step, 256> table = [] {
+            std::array<Step, 256> t{};
+            auto on = [&t](std::initializer_list<uint8_t> ops, Step s) {
+                for (uint8_t o : ops) t[o] = s;
+            };
+            on({0x80}, &PickleMachine::proto);
+            on({0x95}, &PickleMachine::frame);
+            on({'.'}, &PickleMachine::stop);
+            on({'N', 0x88, 0x89}, &PickleMachine::constant);
+            on({'K', 'M', 'J'}, &PickleMachine::binary_int);
+            on({0x8a, 0x8b}, &PickleMachine::long_int);
+            on({'I', 'L'}, &PickleMachine::text_int);
+            on({'G'}, &PickleMachine::binary_float);
+            on({'F'}, &PickleMachine::text_float);
+            on({0x8c, 'X', 0x8d, 'U', 'T'}, &PickleMachine::sized_text);
+            on({'C', 'B', 0x8e, 0x96}, &PickleMachine::sized_bytes);
+            on({'V', 'S'}, &PickleMachine::line_text);
+            on({'(', }, &PickleMachine::mark);
+            on({'0', '1', '2'}, &PickleMachine::stack_op);
+            on({')', 't', 0x85, 0x86, 0x87}, &PickleMachine::make_tuple);
+            on({']', 'l', 0x8f, 0x91}, &PickleMachine::make_list);
+            on({'a', 'e', 0x90}, &PickleMachine::append);
+            on({'}', 'd'}, &PickleMachine::make_dict);
+            on({'s', 'u'}, &PickleMachine::set_items);
+            on({'p', 'q', 'r', 0x94}, &PickleMachine::memo_put);
+            on({'g', 'h', 'j'}, &PickleMachine::memo_get);
+            on({'c', 0x93}, &PickleMachine::global);
+            on({'R', 0x81, 0x92}, &PickleMachine::apply);
+            on({'b'}, &PickleMachine::build);
+            on({'P', 'Q'}, &PickleMachine::persistent);
+            return t;
+        }();
+        return table;
     }
-    uint8_t u8() { return *take(1); }
+
+    // ---- input ----
+    [[noreturn]] void fail(const std::string &what) const {
+        bad("pickle, opcode at byte " + std::to_string(op_at_) + ": " + what);
+    }
+    const uint8_t *span(uint64_t n) {
+        if (n > (uint64_t)(end_ - at_)) fail("the data ends " + std::to_string(n - (uint64_t)(end_ - at_)) +
+                                             " bytes short of this opcode's argument");
+        const uint8_t *p = at_;
+        at_ += n;
+        return p;
+    }
+    uint8_t byte() { return *span(1); }
+    uint64_t unsigned_le(int bytes) {
+        const uint8_t *p = span((uint64_t)bytes);
+        uint64_t v = 0;
+        for (int i = bytes - 1; i >= 0; --i) v = v << 8 | p[i];
+        return v;
+    }
     std::string line() {
-        const uint8_t *q = p_;
-        while (q < end_ && *q != '\n') ++q;
-        if (q >= end_) fail("unterminated line");
-        std::string s(reinterpret_cast<const char *>(p_), q - p_);
-        p_ = q + 1;
-        while (!s.empty() && (s.back() == '\r' || s.back() == ' ')) s.pop_back();
+        const uint8_t *nl = static_cast<const uint8_t *>(std::memchr(at_, '\n', (size_t)(end_ - at_)));
+        if (!nl) fail("a text argument has no terminating newline");
+        std::string s(reinterpret_cast<const char *>(at_), (size_t)(nl - at_));
+        at_ = nl + 1;
         return s;
     }
-    int64_t parse_int(const std::string &t) {
-        char *e = nullptr;
+    int64_t decimal(std::string t) {
+        while (!t.empty() && (t.back() == 'L' || t.back() == ' ' || t.back() == '\r')) t.pop_back();
         errno = 0;
-        const long long v = std::strtoll(t.c_str(), &e, 10);
-        if (t.empty() || *e || errno) fail("bad integer literal `" + t + "`");
-        return v;
+        char *stop = nullptr;
+        const long long v = std::strtoll(t.c_str(), &stop, 10);
+        if (t.empty() || *stop || errno) fail("`" + t + "` is not a 64-bit decimal integer");
+        return (int64_t)v;
     }
-    int64_t long_le(const uint8_t *b, uint64_t n) {
-        if (n == 0) return 0;
-        if (n > 8) fail("integer literal of " + std::to_string(n) + " bytes exceeds 64 bits");
-        uint8_t buf[8];
-        std::memset(buf, (b[n - 1] & 0x80) ? 0xff : 0x00, 8);
-        std::memcpy(buf, b, n);
-        return load_as<int64_t>(buf, false);
-    }
-    void push(PRef v) { stack_.push_back(std::move(v)); }
-    void push_int(int64_t x) {
-        auto v = mk(PVal::Int);
-        v->i = x;
-        push(v);
-    }
-    void push_bool(bool x) {
-        auto v = mk(PVal::Bool);
-        v->i = x;
-        push(v);
-    }
-    void push_str(PVal::Kind k, uint64_t n) {
-        auto v = mk(k);
-        const uint8_t *q = take(n);
-        v->s.assign(reinterpret_cast<const char *>(q), n);
-        push(v);
-    }
-    PRef pop() {
-        if (stack_.empty()) fail("stack underflow");
-        PRef v = stack_.back();
+
+    // ---- the value stack ----
+    void push(PNodeRef n) { stack_.push_back(std::move(n)); }
+    PNodeRef pop() {
+        if (stack_.size() <= floor()) fail("the stack has no value above the last mark");
+        PNodeRef n = std::move(stack_.back());
         stack_.pop_back();
-        return v;
+        return n;
     }
-    PRef top_any() {
-        if (stack_.empty()) fail("stack underflow");
+    PNodeRef &top() {
+        if (stack_.size() <= floor()) fail("the stack has no value above the last mark");
         return stack_.back();
     }
-    PVal *top(PVal::Kind k, const char *op) {
-        if (stack_.empty() || stack_.back()->kind != k) fail(std::string(op) + " on the wrong kind of object");
-        return stack_.back().get();
-    }
-    std::vector<PRef> pop_mark() {
-        if (marks_.empty()) fail("MARK stack underflow");
+    size_t floor() const { return marks_.empty() ? 0 : marks_.back(); }
+    std::vector<PNodeRef> pop_to_mark() {
+        if (marks_.empty()) fail("no mark is set");
         const size_t m = marks_.back();
         marks_.pop_back();
-        if (m > stack_.size()) fail("MARK past the stack");
-        std::vector<PRef> out(stack_.begin() + m, stack_.end());
+        std::vector<PNodeRef> items(std::make_move_iterator(stack_.begin() + (ptrdiff_t)m),
+                                    std::make_move_iterator(stack_.end()));
         stack_.resize(m);
-        return out;
+        return items;
     }
-    std::vector<std::pair<PRef, PRef>> pairs(const std::vector<PRef> &v) {
-        if (v.size() % 2) fail("odd number of items in a dict");
-        std::vector<std::pair<PRef, PRef>> out;
-        for (size_t i = 0; i < v.size(); i += 2) out.emplace_back(v[i], v[i + 1]);
-        return out;
+    PNodeRef whole(int64_t v, PNode::Shape shape = PNode::Shape::Whole) {
+        PNodeRef n = node(shape);
+        n->whole = v;
+        return n;
     }
-    void memoize(uint64_t idx) { memo_[idx] = top_any(); }
-    PRef recall(uint64_t idx) {
-        auto it = memo_.find(idx);
-        if (it == memo_.end()) fail("memo has no entry " + std::to_string(idx));
-        return it->second;
+    PNodeRef text(std::string s, PNode::Shape shape = PNode::Shape::Text) {
+        PNodeRef n = node(shape);
+        n->text = std::move(s);
+        return n;
     }
-    static std::string text(const PRef &v) {
-        if (v->kind != PVal::Str && v->kind != PVal::Bytes) bad("pickle: expected a string");
-        return v->s;
-    }
-    static int64_t integer(const PRef &v) {
-        if (v->kind != PVal::Int && v->kind != PVal::Bool) bad("pickle: expected an integer");
-        return v->i;
-    }
-    static const std::vector<PRef> &seq(const PRef &v) {
-        if (v->kind != PVal::Tuple && v->kind != PVal::List) bad("pickle: expected a tuple");
-        return v->items;
+    // The dict entries of a Table, or of the Apply result SETITEM(S) fill.
+    std::vector<std::pair<PNodeRef, PNodeRef>> &entries_of(PNode &target) {
+        if (target.shape != PNode::Shape::Table && target.shape != PNode::Shape::Apply)
+            fail("items are stored into something that is neither a dict nor a constructed object");
+        return target.table;
     }
 
-    // ('storage', <class or dtype name>, key, location, numel)
-    PRef persistent(const PRef &pid) {
-        const auto &it = seq(pid);
-        if (it.size() < 5 || it[0]->kind != PVal::Str || it[0]->s != "storage") fail("unsupported persistent id");
-        DType t;
-        const std::string cls = it[1]->kind == PVal::Global ? it[1]->s2 : text(it[1]);
-        if (!torch_dtype(cls, t)) fail("unknown storage type " + cls);
-        auto v = mk(PVal::Storage);
-        v->storage.dtype = t;
-        v->storage.key = text(it[2]);
-        v->storage.numel = integer(it[4]);
-        if (v->storage.numel < 0) fail("negative storage size");
-        return v;
+    // ---- steps ----
+    void proto(uint8_t) {
+        if (byte() > 5) fail("protocol above 5");
     }
-
-    PRef reduce(const PRef &fn, const PRef &args) {
-        if (fn->kind != PVal::Global) fail("REDUCE with a callable that is not a global name");
-        const std::string &mod = fn->s, &name = fn->s2;
-        if (mod == "collections" && name == "OrderedDict") {
-            const auto &a = seq(args);
-            auto d = mk(PVal::Dict);
-            if (a.empty()) return d;
-            if (a[0]->kind == PVal::Dict) {
-                d->dict = a[0]->dict;
-            } else if (a[0]->kind == PVal::List || a[0]->kind == PVal::Tuple) {
-                for (const PRef &kv : a[0]->items) {
-                    const auto &p = seq(kv);
-                    if (p.size() != 2) fail("OrderedDict item is not a pair");
-                    d->dict.emplace_back(p[0], p[1]);
-                }
+    void frame(uint8_t) { span(8); }  // frames only group the opcodes that follow
+    void stop(uint8_t) { result_ = pop(); }  // whatever lies below the result is dropped, as CPython does
+    void constant(uint8_t op) {
+        if (op == 'N')
+            push(node(PNode::Shape::Nil));
+        else
+            push(whole(op == 0x88 ? 1 : 0, PNode::Shape::Truth));
+    }
+    void binary_int(uint8_t op) {
+        if (op == 'K') push(whole((int64_t)unsigned_le(1)));
+        if (op == 'M') push(whole((int64_t)unsigned_le(2)));
+        if (op == 'J') push(whole((int64_t)(int32_t)(uint32_t)unsigned_le(4)));
+    }
+    void long_int(uint8_t op) {  // two's complement, little-endian, of the given length
+        const uint64_t n = op == 0x8a ? unsigned_le(1) : unsigned_le(4);
+        if (n > 8) fail("an integer of " + std::to_string(n) + " bytes does not fit 64 bits");
+        uint64_t v = n ? unsigned_le((int)n) : 0;
+        if (n && n < 8 && (v >> (8 * n - 1)) & 1) v |= ~(uint64_t)0 << (8 * n);
+        push(whole((int64_t)v));
+    }
+    void text_int(uint8_t op) {
+        std::string t = line();
+        // In protocol 0 the text "01" / "00" of INT spells True / False.
+        if (op == 'I' && (t == "01" || t == "00"))
+            push(whole(t == "01" ? 1 : 0, PNode::Shape::Truth));
+        else
+            push(whole(decimal(t)));
+    }
+    void binary_float(uint8_t) {
+        PNodeRef n = node(PNode::Shape::Real);
+        n->real = load_as<double>(span(8), true);
+        push(n);
+    }
+    void text_float(uint8_t) {
+        PNodeRef n = node(PNode::Shape::Real);
+        n->real = std::strtod(line().c_str(), nullptr);
+        push(n);
+    }
+    void sized_text(uint8_t op) {
+        const uint64_t n = op == 0x8c || op == 'U' ? unsigned_le(1) : op == 0x8d ? unsigned_le(8) : unsigned_le(4);
+        push(text(std::string(reinterpret_cast<const char *>(span(n)), (size_t)n)));
+    }
+    void sized_bytes(uint8_t op) {
+        const uint64_t n = op == 'C' ? unsigned_le(1) : op == 'B' ? unsigned_le(4) : unsigned_le(8);
+        push(text(std::string(reinterpret_cast<const char *>(span(n)), (size_t)n), PNode::Shape::Raw));
+    }
+    void line_text(uint8_t op) {
+        std::string t = line();
+        // STRING carries a quoted literal; only plain text inside the quotes is kept.
+        if (op == 'S' && t.size() >= 2 && (t[0] == '\'' || t[0] == '"') && t.back() == t[0]) t = t.substr(1, t.size() - 2);
+        push(text(t));
+    }
+    void mark(uint8_t) { marks_.push_back(stack_.size()); }
+    void stack_op(uint8_t op) {
+        if (op == '0') pop();
+        if (op == '1') pop_to_mark();
+        if (op == '2') push(top());
+    }
+    void make_tuple(uint8_t op) {
+        PNodeRef n = node(PNode::Shape::Row);
+        n->tuple = true;
+        if (op == 't') {
+            n->row = pop_to_mark();
+        } else if (op != ')') {
+            const int k = op - 0x84;  // TUPLE1..3
+            n->row.resize((size_t)k);
+            for (int i = k - 1; i >= 0; --i) n->row[(size_t)i] = pop();
+        }
+        push(n);
+    }
+    void make_list(uint8_t op) {  // lists, and sets read as lists
+        PNodeRef n = node(PNode::Shape::Row);
+        if (op == 'l' || op == 0x91) n->row = pop_to_mark();
+        push(n);
+    }
+    void append(uint8_t op) {
+        std::vector<PNodeRef> items;
+        if (op == 'a')
+            items.push_back(pop());
+        else
+            items = pop_to_mark();
+        PNode &list = *top();
+        if (list.shape != PNode::Shape::Row || list.tuple) fail("items are appended to something that is not a list");
+        list.row.insert(list.row.end(), items.begin(), items.end());
+    }
+    void make_dict(uint8_t op) {
+        PNodeRef n = node(PNode::Shape::Table);
+        if (op == 'd') {
+            std::vector<PNodeRef> kv = pop_to_mark();
+            if (kv.size() % 2) fail("a dict is built from an odd number of values");
+            for (size_t i = 0; i < kv.size(); i += 2) n->table.emplace_back(kv[i], kv[i + 1]);
+        }
+        push(n);
+    }
+    void set_items(uint8_t op) {
+        std::vector<PNodeRef> kv;
+        if (op == 's') {
+            PNodeRef v = pop(), k = pop();
+            kv = {k, v};
+        } else {
+            kv = pop_to_mark();
+            if (kv.size() % 2) fail("SETITEMS is given an odd number of values");
+        }
+        auto &dst = entries_of(*top());
+        for (size_t i = 0; i < kv.size(); i += 2) dst.emplace_back(kv[i], kv[i + 1]);
+    }
+    void memo_put(uint8_t op) {
+        const uint64_t slot = op == 'q' ? unsigned_le(1) : op == 'r' ? unsigned_le(4) : op == 'p'
+                                                                              ? (uint64_t)decimal(line())
+                                                                              : (uint64_t)memo_.size();
+        memo_[slot] = top();
+    }
+    void memo_get(uint8_t op) {
+        const uint64_t slot = op == 'h' ? unsigned_le(1) : op == 'j' ? unsigned_le(4) : (uint64_t)decimal(line());
+        const auto it = memo_.find(slot);
+        if (it == memo_.end()) fail("memo slot " + std::to_string(slot) + " is read before it is written");
+        push(it->second);
+    }
+    void global(uint8_t op) {
+        std::string module, qualname;
+        if (op == 'c') {
+            module = line();
+            qualname = line();
+        } else {
+            PNodeRef q = pop(), m = pop();
+            if (m->shape != PNode::Shape::Text || q->shape != PNode::Shape::Text)
+                fail("STACK_GLOBAL needs two strings");
+            module = m->text;
+            qualname = q->text;
+        }
+        push(text(module + "." + qualname, PNode::Shape::Name));  // a name only, never resolved
+    }
+    void apply(uint8_t op) {
+        PNodeRef kwargs = op == 0x92 ? pop() : nullptr;  // NEWOBJ_EX: cls, args, kwargs
+        PNodeRef args = pop(), callee = pop();
+        if (callee->shape != PNode::Shape::Name) fail("a call whose callee is not a global name");
+        if (args->shape != PNode::Shape::Row) fail("a call whose arguments are not a tuple");
+        PNodeRef n = node(PNode::Shape::Apply);
+        n->callee = callee;
+        n->row = args->row;
+        if (kwargs && kwargs->shape == PNode::Shape::Table) n->table = kwargs->table;
+        push(n);
+    }
+    void build(uint8_t) {
+        PNodeRef state = pop();
+        PNode &target = *top();
+        if (target.shape == PNode::Shape::Apply) target.state = state;  // other targets keep no state
+    }
+    void persistent(uint8_t op) {
+        PNodeRef n = node(PNode::Shape::Persistent);
+        if (op == 'Q') {
+            PNodeRef id = pop();
+            if (id->shape != PNode::Shape::Row) fail("a persistent id that is not a tuple");
+            n->row = id->row;
+        } else {
+            n->row = repr_tuple(line());
+        }
+        push(n);
+    }
+    // PERSID carries the id as the text of a Python tuple, e.g.
+    // ('storage', <class 'torch.FloatStorage'>, '0', 'cpu', 2): quoted
+    // strings, <class '...'> names and decimal integers are read.
+    std::vector<PNodeRef> repr_tuple(const std::string &t) {
+        std::vector<PNodeRef> items;
+        size_t i = t.find('(');
+        if (i == std::string::npos) fail("a text persistent id that is not a tuple");
+        ++i;
+        while (i < t.size() && t[i] != ')') {
+            while (i < t.size() && (t[i] == ' ' || t[i] == ',')) ++i;
+            if (i >= t.size() || t[i] == ')') break;
+            if (t[i] == '\'' || t[i] == '"') {
+                const size_t close = t.find(t[i], i + 1);
+                if (close == std::string::npos) fail("an unterminated string in a persistent id");
+                items.push_back(text(t.substr(i + 1, close - i - 1)));
+                i = close + 1;
+            } else if (t.compare(i, 8, "<class '") == 0) {
+                const size_t close = t.find("'>", i + 8);
+                if (close == std::string::npos) fail("an unterminated class name in a persistent id");
+                items.push_back(text(t.substr(i + 8, close - i - 8), PNode::Shape::Name));
+                i = close + 2;
             } else {
-                fail("OrderedDict from an unsupported value");
+                const size_t stop = t.find_first_of(",)", i);
+                items.push_back(whole(decimal(t.substr(i, stop == std::string::npos ? std::string::npos : stop - i))));
+                i = stop == std::string::npos ? t.size() : stop;
             }
-            return d;
         }
-        if (mod == "torch._utils" &&
-            (name == "_rebuild_tensor_v2" || name == "_rebuild_tensor" || name == "_rebuild_tensor_v3")) {
-            const auto &a = seq(args);
-            if (a.size() < 4) fail("_rebuild_tensor with too few arguments");
-            if (a[0]->kind != PVal::Storage) fail("_rebuild_tensor without a storage");
-            auto v = mk(PVal::Tensor);
-            v->tensor.storage = a[0]->storage;
-            v->tensor.offset = integer(a[1]);
-            if (v->tensor.offset < 0) fail("negative storage offset");
-            if (a[2]->kind == PVal::Tuple && a[3]->kind == PVal::Tuple) {
-                v->tensor.dense = true;
-                for (const PRef &d : a[2]->items) v->tensor.size.push_back(integer(d));
-                for (const PRef &d : a[3]->items) v->tensor.stride.push_back(integer(d));
-                if (v->tensor.size.size() != v->tensor.stride.size()) fail("size and stride ranks differ");
-            }
-            return v;
-        }
-        if (mod == "torch._utils" && (name == "_rebuild_parameter" || name == "_rebuild_parameter_with_state")) {
-            const auto &a = seq(args);
-            if (a.empty()) fail("_rebuild_parameter without arguments");
-            return a[0];
-        }
-        auto v = mk(PVal::Opaque);
-        v->s = mod + "." + name;
-        return v;
+        return items;
     }
+
+    const uint8_t *begin_, *at_, *end_;
+    size_t op_at_ = 0;
+    std::vector<PNodeRef> stack_;
+    std::vector<size_t> marks_;
+    std::map<uint64_t, PNodeRef> memo_;
+    PNodeRef result_;
 };
 
-bool looks_like_state_dict(const PVal &d) {
-    for (const auto &kv : d.dict)
-        if (kv.second->kind == PVal::Tensor && kv.second->tensor.dense) return true;
+// ----- torch's objects in an evaluated pickle -----
+
+// A storage's element type from its class name ("torch.HalfStorage") or
+// dtype name ("torch.float16"): the part between "torch." and "Storage",
+// lower-cased, names the element type.
+bool torch_element_type(std::string s, DType &t) {
+    std::transform(s.begin(), s.end(), s.begin(), [](unsigned char ch) { return (char)std::tolower(ch); });
+    if (s.rfind("torch.", 0) == 0) s.erase(0, 6);
+    if (s.size() > 7 && s.compare(s.size() - 7, 7, "storage") == 0) s.erase(s.size() - 7);
+    static const std::map<std::string, DType> types = {
+        {"bool", DType::Bool},   {"byte", DType::U8},      {"uint8", DType::U8},    {"char", DType::I8},
+        {"int8", DType::I8},     {"short", DType::I16},    {"int16", DType::I16},   {"int", DType::I32},
+        {"int32", DType::I32},   {"long", DType::I64},     {"int64", DType::I64},   {"half", DType::F16},
+        {"float16", DType::F16}, {"bfloat16", DType::BF16}, {"float", DType::F32},  {"float32", DType::F32},
+        {"double", DType::F64},  {"float64", DType::F64}};
+    const auto it = types.find(s);
+    if (it == types.end()) return false;
+    t = it->second;
+    return true;
+}
+
+struct TorchStorage {
+    DType type = DType::F32;
+    std::string key;  // archive entry <root>/data/<key>
+    int64_t numel = 0;
+};
+
+struct TorchTensor {
+    TorchStorage storage;
+    int64_t offset = 0;
+    std::vector<int64_t> size, stride;
+};
+
+bool is_call(const PNode &n, const char *name) {
+    return n.shape == PNode::Shape::Apply && n.callee && n.callee->text == name;
+}
+
+std::vector<int64_t> whole_list(const PNode &n, const std::string &what) {
+    if (n.shape != PNode::Shape::Row) bad("torch tensor: " + what + " is not a tuple");
+    std::vector<int64_t> out;
+    for (const PNodeRef &x : n.row) {
+        if (x->shape != PNode::Shape::Whole) bad("torch tensor: " + what + " holds a value that is not an integer");
+        out.push_back(x->whole);
+    }
+    return out;
+}
+
+// The storage a persistent id ("storage", <storage class>, key, location,
+// numel) points at.
+TorchStorage torch_storage(const PNode &id) {
+    if (id.shape != PNode::Shape::Persistent || id.row.size() < 5 || id.row[0]->shape != PNode::Shape::Text ||
+        id.row[0]->text != "storage")
+        bad("torch tensor: its storage is not a (\"storage\", class, key, location, size) reference");
+    const PNode &cls = *id.row[1], &key = *id.row[2], &numel = *id.row[4];
+    TorchStorage s;
+    if (cls.shape != PNode::Shape::Name || !torch_element_type(cls.text, s.type))
+        bad("torch tensor: storage class `" + cls.text + "` has no element type this reader knows");
+    if (key.shape != PNode::Shape::Text) bad("torch tensor: the storage key is not a string");
+    if (numel.shape != PNode::Shape::Whole || numel.whole < 0) bad("torch tensor: the storage size is not a count");
+    s.key = key.text;
+    s.numel = numel.whole;
+    return s;
+}
+
+// A dense tensor value: _rebuild_tensor(_v2)(storage, offset, size, stride,
+// ...), possibly wrapped in _rebuild_parameter(tensor, requires_grad, hooks).
+// Returns false for every other value.
+bool torch_tensor(const PNode &n, TorchTensor &t) {
+    if (is_call(n, "torch._utils._rebuild_parameter") || is_call(n, "torch._utils._rebuild_parameter_with_state"))
+        return !n.row.empty() && torch_tensor(*n.row[0], t);
+    if (!is_call(n, "torch._utils._rebuild_tensor_v2") && !is_call(n, "torch._utils._rebuild_tensor")) return false;
+    if (n.row.size() < 4) bad("torch tensor: the rebuild call has fewer than four arguments");
+    t.storage = torch_storage(*n.row[0]);
+    if (n.row[1]->shape != PNode::Shape::Whole || n.row[1]->whole < 0)
+        bad("torch tensor: the storage offset is not a count");
+    t.offset = n.row[1]->whole;
+    t.size = whole_list(*n.row[2], "the size");
+    t.stride = whole_list(*n.row[3], "the stride");
+    if (t.size.size() != t.stride.size()) bad("torch tensor: size and stride have different lengths");
+    return true;
+}
+
+// Torch's rebuild functions this reader does not read (sparse, quantized,
+// meta, ...): a state-dict entry made by one of them is an error, not skipped.
+bool unreadable_torch_tensor(const PNode &n) {
+    return n.shape == PNode::Shape::Apply && n.callee && n.callee->text.rfind("torch._utils._rebuild_", 0) == 0;
+}
+
+// The (key, value) entries of a mapping: a dict, or an OrderedDict call
+// (given its items as an argument, filled by SETITEMS, or both).
+bool mapping_entries(const PNode &n, std::vector<std::pair<PNodeRef, PNodeRef>> &out) {
+    out.clear();
+    if (n.shape == PNode::Shape::Table) {
+        out = n.table;
+        return true;
+    }
+    if (!is_call(n, "collections.OrderedDict")) return false;
+    if (!n.row.empty()) {
+        const PNode &items = *n.row[0];
+        if (items.shape == PNode::Shape::Table) {
+            out = items.table;
+        } else if (items.shape == PNode::Shape::Row) {
+            for (const PNodeRef &pair : items.row) {
+                if (pair->shape != PNode::Shape::Row || pair->row.size() != 2)
+                    bad("checkpoint: an OrderedDict item is not a (key, value) pair");
+                out.emplace_back(pair->row[0], pair->row[1]);
+            }
+        } else {
+            bad("checkpoint: OrderedDict is built from a value that holds no items");
+        }
+    }
+    out.insert(out.end(), n.table.begin(), n.table.end());
+    return true;
+}
+
+bool holds_a_tensor(const std::vector<std::pair<PNodeRef, PNodeRef>> &entries) {
+    TorchTensor t;
+    for (const auto &kv : entries)
+        if (torch_tensor(*kv.second, t)) return true;
     return false;
 }
 
+// The state dict of a checkpoint: the top-level mapping itself, or its
+// "model_state_dict", "state_dict" or "state" entry (a training checkpoint or
+// a demucs package around it) -- whichever first holds a tensor.
+std::vector<std::pair<PNodeRef, PNodeRef>> find_state_dict(const PNode &top) {
+    std::vector<std::pair<PNodeRef, PNodeRef>> entries, inner;
+    if (!mapping_entries(top, entries)) bad("checkpoint: the pickled object is not a dict");
+    for (const char *wrapper : {"model_state_dict", "state_dict", "state"})
+        for (const auto &kv : entries)
+            if (kv.first->shape == PNode::Shape::Text && kv.first->text == wrapper &&
+                mapping_entries(*kv.second, inner) && holds_a_tensor(inner))
+                return inner;
+    if (holds_a_tensor(entries)) return entries;
+    bad("checkpoint: neither the pickled dict nor a model_state_dict / state_dict / state entry of it holds a tensor");
+}
+
+// A tensor's values as f32, read through its size and stride from the
+// storage's bytes.
+Tensor gather(const std::string &name, const TorchTensor &t, const uint8_t *blob, uint64_t blob_bytes, bool big) {
+    const int es = dtype_size(t.storage.type);
+    if (blob_bytes % (uint64_t)es) bad("checkpoint: storage " + t.storage.key + " is not a whole number of elements");
+    if ((uint64_t)t.storage.numel > blob_bytes / (uint64_t)es)
+        bad("checkpoint: storage " + t.storage.key + " is declared with " + std::to_string(t.storage.numel) +
+            " elements but its entry holds " + std::to_string(blob_bytes / (uint64_t)es));
+    Tensor out;
+    out.shape = t.size;
+    const uint64_t n = checked_product(out.shape, name);
+    out.data.resize(n);
+    if (n == 0) return out;
+    // Highest storage index the view touches: offset + sum (size_d - 1) stride_d.
+    int64_t last = t.offset;
+    for (size_t d = 0; d < t.size.size(); ++d) {
+        if (t.stride[d] < 0) bad("checkpoint: tensor `" + name + "` has a negative stride");
+        if (t.size[d] > 1 && t.stride[d] > (std::numeric_limits<int64_t>::max() - last) / (t.size[d] - 1))
+            bad("checkpoint: tensor `" + name + "` reaches past the end of its storage");
+        last += (t.size[d] - 1) * t.stride[d];
+    }
+    if (last >= t.storage.numel) bad("checkpoint: tensor `" + name + "` reaches past the end of its storage");
+    // Row-major walk; the innermost dimension is decoded as one strided run.
+    const size_t rank = t.size.size();
+    const int64_t inner = rank ? t.size[rank - 1] : 1, inner_stride = rank ? t.stride[rank - 1] : 1;
+    std::vector<int64_t> idx(rank ? rank - 1 : 0, 0);
+    for (uint64_t at_out = 0; at_out < n; at_out += (uint64_t)inner) {
+        int64_t base = t.offset;
+        for (size_t d = 0; d + 1 < rank; ++d) base += idx[d] * t.stride[d];
+        if (inner_stride == 1) {
+            decode(blob + (uint64_t)base * es, (size_t)inner, t.storage.type, big, &out.data[at_out]);
+        } else {
+            for (int64_t i = 0; i < inner; ++i)
+                decode(blob + (uint64_t)(base + i * inner_stride) * es, 1, t.storage.type, big, &out.data[at_out + i]);
+        }
+        for (size_t d = idx.size(); d-- > 0;) {
+            if (++idx[d] < t.size[d]) break;
+            idx[d] = 0;
+        }
+    }
+    return out;
+}
+
+// A torch.save archive: "<root>/data.pkl", one "<root>/data/<key>" entry per
+// storage, and "<root>/byteorder" ("little" when absent).
 void parse_torch_zip(const uint8_t *z, size_t len, dmx_checkpoint &c) {
     const auto dir = zip_directory(z, len);
-    std::string root;
-    bool found = false;
-    for (const auto &e : dir) {
-        const std::string &n = e.first;
-        if (n.size() >= 9 && n.compare(n.size() - 9, 9, "/data.pkl") == 0) {
-            root = n.substr(0, n.size() - 9);
-            found = true;
+    const std::string suffix = "/data.pkl";
+    auto pkl = dir.end();
+    for (auto it = dir.begin(); it != dir.end(); ++it)
+        if (it->first.size() > suffix.size() &&
+            it->first.compare(it->first.size() - suffix.size(), suffix.size(), suffix) == 0) {
+            pkl = it;
             break;
         }
-    }
-    if (!found) bad("archive contains no `<root>/data.pkl`; is this a torch.save file?");
+    if (pkl == dir.end()) bad("checkpoint: the archive has no `<root>/data.pkl` entry; it is not a torch.save file");
+    const std::string root = pkl->first.substr(0, pkl->first.size() - suffix.size());
     bool big = false;
-    if (auto bo = dir.find(root + "/byteorder"); bo != dir.end()) {
-        auto d = zip_data(z, len, bo->second, bo->first);
-        std::string s(reinterpret_cast<const char *>(d.first), d.second);
-        while (!s.empty() && (s.back() == '\n' || s.back() == ' ' || s.back() == '\r')) s.pop_back();
-        big = s == "big";
+    if (const auto bo = dir.find(root + "/byteorder"); bo != dir.end()) {
+        const auto d = zip_data(z, len, bo->second, bo->first);
+        big = std::string(reinterpret_cast<const char *>(d.first), (size_t)d.second).rfind("big", 0) == 0;
     }
-    auto pk = dir.find(root + "/data.pkl");
-    auto pkd = zip_data(z, len, pk->second, pk->first);
-    const PRef top = Unpickler(pkd.first, pkd.second).run();
-    if (top->kind != PVal::Dict) bad("checkpoint top level is not a dict");
-    const PVal *state = nullptr;
-    for (const char *key : {"model_state_dict", "state_dict", "state"}) {
-        for (const auto &kv : top->dict)
-            if (kv.first->kind == PVal::Str && kv.first->s == key && kv.second->kind == PVal::Dict &&
-                looks_like_state_dict(*kv.second)) {
-                state = kv.second.get();
-                break;
-            }
-        if (state) break;
-    }
-    if (!state && looks_like_state_dict(*top)) state = top.get();
-    if (!state) bad("checkpoint has no tensor state dict (looked for model_state_dict/state_dict/state)");
-    for (const auto &kv : state->dict) {
-        if (kv.first->kind != PVal::Str) bad("state dict key is not a string");
-        const std::string &name = kv.first->s;
-        const PVal &v = *kv.second;
-        if (v.kind == PVal::None || v.kind == PVal::Opaque) continue;
-        if (v.kind != PVal::Tensor) bad("state dict entry `" + name + "` is not a tensor");
-        if (!v.tensor.dense) bad("tensor `" + name + "` is sparse, which is not supported");
-        const TensorRef &t = v.tensor;
-        auto se = dir.find(root + "/data/" + t.storage.key);
-        if (se == dir.end()) bad("missing archive entry " + root + "/data/" + t.storage.key);
-        auto blob = zip_data(z, len, se->second, se->first);
-        const int es = dtype_size(t.storage.dtype);
-        if (blob.second % es) bad("storage " + t.storage.key + " length is not a multiple of its element size");
-        const uint64_t avail = blob.second / es;
-        if ((uint64_t)t.storage.numel > avail)
-            bad("storage " + t.storage.key + " holds " + std::to_string(avail) + " elements but is declared with " +
-                std::to_string(t.storage.numel));
-        Tensor out;
-        out.shape = t.size;
-        const uint64_t n = checked_product(out.shape, name);
-        out.data.resize(n);
-        bool contiguous = true;
-        for (int64_t d = (int64_t)out.shape.size() - 1, acc = 1; d >= 0; acc *= out.shape[d], --d)
-            if (out.shape[d] != 1 && t.stride[d] != acc) contiguous = false;
-        if (contiguous) {
-            if ((uint64_t)t.offset + n > (uint64_t)t.storage.numel) bad("tensor `" + name + "` reads past its storage");
-            decode(blob.first + (uint64_t)t.offset * es, n, t.storage.dtype, big, out.data.data());
-            c.tensors[name] = std::move(out);
-            continue;
+    const auto program = zip_data(z, len, pkl->second, pkl->first);
+    const PNodeRef top = PickleMachine(program.first, (size_t)program.second).evaluate();
+    for (const auto &kv : find_state_dict(*top)) {
+        if (kv.first->shape != PNode::Shape::Text) bad("checkpoint: a state-dict key is not a string");
+        const std::string &name = kv.first->text;
+        TorchTensor t;
+        if (!torch_tensor(*kv.second, t)) {
+            if (unreadable_torch_tensor(*kv.second))
+                bad("checkpoint: tensor `" + name + "` is stored by " + kv.second->callee->text +
+                    ", which this reader does not read (only dense tensors)");
+            const PNode::Shape sh = kv.second->shape;
+            if (sh == PNode::Shape::Nil || sh == PNode::Shape::Apply || sh == PNode::Shape::Name) continue;
+            bad("checkpoint: state-dict entry `" + name + "` is a plain value, not a tensor");
         }
-        // Element (i_0..i_k) sits at offset + sum i_d stride_d of the storage.
-        std::vector<int64_t> idx(out.shape.size(), 0);
-        for (uint64_t e = 0; e < n; ++e) {
-            int64_t at = t.offset;
-            for (size_t d = 0; d < idx.size(); ++d) at += idx[d] * t.stride[d];
-            if (at < 0 || (uint64_t)at >= (uint64_t)t.storage.numel) bad("tensor `" + name + "` reads past its storage");
-            decode(blob.first + (uint64_t)at * es, 1, t.storage.dtype, big, &out.data[e]);
-            for (size_t d = idx.size(); d-- > 0;) {
-                if (++idx[d] < out.shape[d]) break;
-                idx[d] = 0;
-            }
-        }
-        c.tensors[name] = std::move(out);
+        const auto blob = dir.find(root + "/data/" + t.storage.key);
+        if (blob == dir.end()) bad("checkpoint: the archive lacks the storage entry " + root + "/data/" + t.storage.key);
+        const auto bytes = zip_data(z, len, blob->second, blob->first);
+        c.tensors[name] = gather(name, t, bytes.first, bytes.second, big);
     }
 }
 

@@ -289,25 +289,37 @@ struct Branches {
     }
 };
 
-// `HtdemucsConfig::validate` (crates/demucs-core/src/demucs/config.rs:239-273).
+// The configurations the kernels are written for; anything else is refused
+// with the UnsupportedModel kind rather than computed wrongly (the same set
+// HtdemucsConfig::validate admits, crates/demucs-core/src/demucs/config.rs:239-273).
 void validate(const dmx_config &c) {
-    auto unsupported = [](const char *what) {
-        throw_error(DMX_ERR_UNSUPPORTED, std::string("htdemucs config: ") + what + " is not supported by this port");
-    };
-    if (!c.cac) unsupported("cac = false (magnitude masking)");
-    if (c.nfft != 4096) unsupported("nfft != 4096");
-    if (c.kernel_size != 8 || c.stride != 4) unsupported("kernel_size/stride other than 8/4");
-    if (c.audio_channels != 2) unsupported("audio_channels != 2");
-    if (c.sources != 4) unsupported("a source count other than 4");
-    int freqs = c.nfft / 2;
-    for (int i = 0; i < c.depth; ++i) {
-        if (freqs > 1 && freqs <= c.kernel_size) unsupported("a `last_freq` layer");
-        if (freqs > 1) freqs /= c.stride;
+    // The spectral branch keeps more than one bin through every encoder level
+    // (a level whose input has at most kernel_size bins would merge the two
+    // branches inside the encoder, which this backend does not build).
+    bool bins_survive = true;
+    for (int i = 0, f = c.nfft / 2; i < c.depth; ++i) {
+        if (f > 1 && f <= c.kernel_size) bins_survive = false;
+        if (f > 1) f /= std::max(c.stride, 1);
     }
-    if (c.context != 1) unsupported("context != 1");
-    if (c.bottom_channels <= 0) unsupported("bottom_channels = 0");
-    if (c.t_heads <= 0 || c.bottom_channels % c.t_heads || c.bottom_channels / c.t_heads != 64)
-        unsupported("a head width other than 64");
+    const struct {
+        bool ok;
+        const char *needs;
+    } rules[] = {
+        {c.cac != 0, "complex-as-channels spectrograms (cac = true)"},
+        {c.nfft == 4096, "nfft = 4096"},
+        {c.kernel_size == 8 && c.stride == 4, "encoder kernel 8 with stride 4"},
+        {c.audio_channels == 2, "stereo audio"},
+        {c.sources == 4, "four sources"},
+        {bins_survive, "frequency bins left after every encoder level"},
+        {c.context == 1, "context = 1"},
+        {c.bottom_channels > 0, "a transformer width (bottom_channels > 0)"},
+        {c.t_heads > 0 && c.bottom_channels % std::max(c.t_heads, 1) == 0 &&
+             c.bottom_channels / std::max(c.t_heads, 1) == 64,
+         "attention heads 64 wide"},
+    };
+    for (const auto &rule : rules)
+        if (!rule.ok) throw_error(DMX_ERR_UNSUPPORTED, std::string("unsupported htdemucs configuration: this backend needs ") +
+                                                           rule.needs);
     if (c.segment <= 0.0) throw_error(DMX_ERR_CONFIG, "segment must be positive");
 }
 

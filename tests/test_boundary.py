@@ -29,3 +29,21 @@ def test_every_declared_function_is_exported_and_bound():
     extra = sorted(set(_native.SIGNATURES) - declared)
     assert not extra, extra
     _native.load()  # binds every signature
+
+
+def test_unsupported_configurations_are_refused_before_any_device_work():
+    """dmx_runner_create checks the config first (UnsupportedModel / Config
+    kinds), so these errors need no GPU; the weights are never looked at."""
+    import pytest
+    pkg = load_package()
+    cases = [dict(cac=0), dict(nfft=2048), dict(stride=2), dict(sources=6), dict(depth=6), dict(t_heads=4),
+             dict(context=0)]
+    for change in cases:
+        cfg = pkg.Config(**change)
+        with pytest.raises(pkg.DmxError) as e:
+            pkg.Runner({}, cfg)
+        assert e.value.kind == "UnsupportedModel", change
+        assert "this backend needs" in str(e.value)
+    with pytest.raises(pkg.DmxError) as e:
+        pkg.Runner({}, pkg.Config(segment=0.0))
+    assert e.value.kind == "Config"

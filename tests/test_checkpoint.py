@@ -131,6 +131,34 @@ def test_torch_zip_state_dicts_are_read_through_the_pickle(ckpt, wrap):
     assert loaded.metadata == {} and loaded.config == pkg.Config()
 
 
+@pytest.mark.parametrize("protocol", [0, 1, 3, 4, 5])
+def test_every_pickle_protocol_torch_writes_is_read(ckpt, protocol):
+    """torch.save(pickle_protocol=p): protocol 0/1 text opcodes (INT, GET,
+    PUT, GLOBAL lines), protocol 4/5 frames, MEMOIZE and STACK_GLOBAL."""
+    _, ck = ckpt
+    sd = state_dict()
+    buf = io.BytesIO()
+    torch.save(sd, buf, pickle_protocol=protocol)
+    loaded = ck.load_weights_from_bytes(buf.getvalue(), torch_zip=True)
+    assert list(loaded.tensors) == sorted(sd)
+    for name, t in sd.items():
+        np.testing.assert_array_equal(loaded.tensors[name], expected(t), err_msg=name)
+
+
+def test_non_tensor_entries_are_skipped_and_sparse_tensors_refused(ckpt):
+    _, ck = ckpt
+    sd = OrderedDict(w=torch.ones(2), none=None, obj=Fraction(1, 3))
+    loaded = ck.load_weights_from_bytes(torch_bytes(sd), torch_zip=True)
+    assert list(loaded.tensors) == ["w"]
+    sp = torch.sparse_coo_tensor([[0, 1], [1, 0]], [1.0, 2.0], (2, 2))
+    with pytest.raises(ck.CheckpointError) as e:
+        ck.load_weights_from_bytes(torch_bytes(OrderedDict(w=torch.ones(2), s=sp)), torch_zip=True)
+    assert e.value.code == CHECKPOINT and "only dense tensors" in str(e.value)
+    with pytest.raises(ck.CheckpointError) as e:
+        ck.load_weights_from_bytes(torch_bytes(OrderedDict(w=torch.ones(2), n=3)), torch_zip=True)
+    assert "plain value" in str(e.value)
+
+
 def test_torch_zip_file_by_extension(ckpt, tmp_path):
     _, ck = ckpt
     sd = state_dict()
@@ -167,14 +195,14 @@ def st_raw(header, data=b""):
 
 
 @pytest.mark.parametrize("data,message", [
-    (b"\x01\x02\x03", "shorter than its header length"),
-    (struct.pack("<Q", 1000) + b"{}", "header claims 1000 bytes"),
+    (b"\x01\x02\x03", "cannot hold the 8-byte header size"),
+    (struct.pack("<Q", 1000) + b"{}", "announces 1000 bytes"),
     (struct.pack("<Q", 5) + b"{oops", "JSON"),
-    (st_raw({"x": {"dtype": "F32", "shape": [3], "data_offsets": [0, 8]}}, b"\0" * 8), "do not match"),
-    (st_raw({"x": {"dtype": "F32", "shape": [1], "data_offsets": [4, 8]}}, b"\0" * 4), "outside the 4 data bytes"),
-    (st_raw({"x": {"dtype": "F8_E4M3", "shape": [1], "data_offsets": [0, 1]}}, b"\0"), "unsupported safetensors dtype"),
-    (st_raw({"x": {"shape": [1], "data_offsets": [0, 4]}}, b"\0" * 4), "no dtype"),
-    (st_raw({"x": {"dtype": "F32", "shape": [1], "data_offsets": [0]}}, b"\0" * 4), "malformed data_offsets"),
+    (st_raw({"x": {"dtype": "F32", "shape": [3], "data_offsets": [0, 8]}}, b"\0" * 8), "takes 12 bytes, but its entry spans 8"),
+    (st_raw({"x": {"dtype": "F32", "shape": [1], "data_offsets": [4, 8]}}, b"\0" * 4), "lie beyond the 4-byte data section"),
+    (st_raw({"x": {"dtype": "F8_E4M3", "shape": [1], "data_offsets": [0, 1]}}, b"\0"), "element type `F8_E4M3`"),
+    (st_raw({"x": {"shape": [1], "data_offsets": [0, 4]}}, b"\0" * 4), "lacks a `dtype` string"),
+    (st_raw({"x": {"dtype": "F32", "shape": [1], "data_offsets": [0]}}, b"\0" * 4), "must be the pair [begin, end]"),
 ])
 def test_malformed_safetensors_are_checkpoint_errors(ckpt, data, message):
     _, ck = ckpt
@@ -193,10 +221,10 @@ def zip_bytes(entries, method=zipfile.ZIP_STORED):
 
 @pytest.mark.parametrize("data,message", [
     (b"not a zip at all, but long enough to scan", "not a zip archive"),
-    (zip_bytes({"archive/other": b"x"}), "no `<root>/data.pkl`"),
-    (zip_bytes({"archive/data.pkl": pickle.dumps({"a": 1}, protocol=2)}), "no tensor state dict"),
-    (zip_bytes({"archive/data.pkl": b"\x80\x02\xff."}), "unsupported pickle opcode 0xff"),
-    (zip_bytes({"archive/data.pkl": b"\x80\x02}q\x00(X\x01\x00\x00\x00a"}), "truncated"),
+    (zip_bytes({"archive/other": b"x"}), "no `<root>/data.pkl` entry"),
+    (zip_bytes({"archive/data.pkl": pickle.dumps({"a": 1}, protocol=2)}), "holds a tensor"),
+    (zip_bytes({"archive/data.pkl": b"\x80\x02\xff."}), "opcode 0xff is not one this reader runs"),
+    (zip_bytes({"archive/data.pkl": b"\x80\x02}q\x00(X\x01\x00\x00\x00a"}), "ends before a STOP opcode"),
     (zip_bytes({"archive/data.pkl": pickle.dumps({"a": 1}, protocol=2)}, zipfile.ZIP_DEFLATED), "compressed"),
 ])
 def test_malformed_torch_zips_are_checkpoint_errors(ckpt, data, message):
@@ -212,7 +240,7 @@ def test_a_missing_storage_blob_is_reported(ckpt):
     kept = {n: src.read(n) for n in src.namelist() if "/data/" not in n}
     with pytest.raises(ck.CheckpointError) as e:
         ck.load_weights_from_bytes(zip_bytes(kept), torch_zip=True)
-    assert "missing archive entry" in str(e.value)
+    assert "lacks the storage entry" in str(e.value)
 
 
 def test_a_missing_file_is_an_io_error(ckpt, tmp_path):
