@@ -354,6 +354,64 @@ def segment_forward_path(pkg, runner, mix, batch_chunks: int, ref_stems, repeats
                     f"{repeats} after a warm-up"}
 
 
+def profile_workload(pkg, torch, args):
+    """One workload alone, for rocprofv3 (kernel trace, memory-copy trace or
+    counters): `--warmup` untimed and `--steps` timed calls, then the copy
+    that calibrates FETCH_SIZE / WRITE_SIZE. Returns the wall time per call."""
+    cfg = pkg.Config()
+    lib = pkg._native.load()
+    if args.profile == "bf16":
+        batch = 32
+        runner = pkg.Runner(pkg.random_init(7, cfg), cfg, precision=pkg.PRECISION_BF16)
+        L = cfg.training_length
+        d_mix = torch.from_numpy(pkg.signals.gaussian_segments(7, batch, L)).cuda()
+        d_out = torch.empty((batch, cfg.sources, 2, L), device="cuda")
+
+        def call():
+            rc = lib.dmx_forward_device(runner.handle, ctypes.c_void_p(d_mix.data_ptr()), batch, 2, L,
+                                        ctypes.c_void_p(d_out.data_ptr()))
+            if rc != 0:
+                raise RuntimeError(pkg._native.last_error())
+        what = f"config 5: bf16 forward of {batch} segments (dmx_forward_device)"
+    else:
+        runner = pkg.Runner(pkg.random_init(0, cfg), cfg)
+        mix = pkg.signals.synthetic_mix(0, args.seconds)
+        samples = mix.shape[1]
+        opts = pkg.SeparateOptions(shifts=0, overlap=0.25, batch_chunks=args.batch_chunks)
+        if args.profile == "host":
+            left, right = np.ascontiguousarray(mix[0]), np.ascontiguousarray(mix[1])
+
+            def call():
+                pkg.separate_runners([runner], left, right, cfg.samplerate, opts)
+            what = f"config 3: {args.seconds:g} s separation, host arrays in and out (dmx_separate)"
+        else:
+            d_mix = torch.from_numpy(mix).cuda()
+            d_stems = torch.empty((cfg.sources, 2, samples), device="cuda")
+            c_opts = opts.to_c()
+            handles = (ctypes.c_void_p * 1)(runner.handle)
+
+            def call():
+                rc = lib.dmx_separate_device(handles, None, 1, None, ctypes.c_void_p(d_mix.data_ptr()), samples,
+                                             cfg.samplerate, ctypes.byref(c_opts), pkg._native.PROGRESS(), None,
+                                             ctypes.c_void_p(d_stems.data_ptr()))
+                if rc != 0:
+                    raise RuntimeError(pkg._native.last_error())
+            what = f"config 3: {args.seconds:g} s separation, mix and stems in HBM (dmx_separate_device)"
+    for _ in range(args.warmup):
+        call()
+    runner.synchronize()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        call()
+    runner.synchronize()
+    torch.cuda.synchronize()
+    ms = 1000.0 * (time.perf_counter() - t0) / max(1, args.steps)
+    mib = copy_calibration(torch)
+    return {"profile": args.profile, "workload": what, "warmup": args.warmup, "steps": args.steps,
+            "ms_per_call": round(ms, 3), "copy_calibration_mib": mib}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -367,6 +425,11 @@ def main():
                     help="only the roofline kernel loop and the copy calibration (for rocprofv3 runs)")
     ap.add_argument("--no-other-configs", action="store_true",
                     help="skip the config 2 / 4 / 5 measurements reported beside the headline")
+    ap.add_argument("--profile", choices=("host", "device", "bf16"),
+                    help="for rocprofv3 runs: only --warmup + --steps of one workload and one short JSON line: "
+                         "host = the config-3 separation from host arrays (dmx_separate), device = the same with "
+                         "mix and stems in HBM (dmx_separate_device), bf16 = the config-5 forward of 32 segments; "
+                         "each followed by the 256 MiB copy that calibrates the traffic counters")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py: this build runs on one GPU only; multi-GPU runs are not part of it "
@@ -382,6 +445,9 @@ def main():
         print(json.dumps({"kernel": "attention_kernel", "avg_ms": round(attn_ms, 4),
                           "tflops": round(attn_flops / (attn_ms * 1e-3) / 1e12, 2),
                           "flops_per_launch": attn_flops, "copy_calibration_mib": mib}))
+        return
+    if args.profile:
+        print(json.dumps(profile_workload(pkg, torch, args)))
         return
     cfg = pkg.Config()
     weights = pkg.random_init(0, cfg)

@@ -1,6 +1,7 @@
 // norm.hip — LayerNorm, GroupNorm and the elementwise ops of the forward.
 // HBM-bound: each kernel reads and writes its tensor once, float4 where the
 // layout allows, with wave64 shuffle reductions.
+
 #include "common.h"
 #include "ops.h"
 
@@ -80,43 +81,112 @@ __global__ __launch_bounds__(256) void layer_norm_vec_kernel(const float4 *__res
 }
 
 // (b, c, F*T) channel-major -> LayerNorm'd token rows (b, T*F, c), token = t*F + f,
-// plus pos[token] * pos_weight. A block gathers 16 positions x all channels
-// through LDS so both the read and the write are coalesced.
-constexpr int TOK_POS = 16;
-__global__ __launch_bounds__(256) void channels_to_tokens_ln_kernel(const float *__restrict__ x, int c, int F, int T,
-                                                                    const float *__restrict__ w,
-                                                                    const float *__restrict__ bias,
-                                                                    const float *__restrict__ pos, float pos_weight,
-                                                                    float *__restrict__ out) {
+// plus pos[token] * pos_weight. A block stages TOK_POS positions x all
+// channels in LDS ([c][TOK_POS + 1]: an odd row stride, so a wave reading one
+// position across 64 channels hits 64 distinct banks), reading each channel's
+// run of TOK_POS floats as float4s, then writes whole token rows. Blocks are handed to the 8 XCDs round-robin; the work list is
+// (position block, batch row) with the batch row fastest and each XCD takes a
+// contiguous range of it, so the batch rows of a position block run on one
+// XCD and read that block's positional rows into one L2.
+constexpr int TOK_XCDS = 8;
+// CK = c / 64 when c is a multiple of 64 up to 512 (the model's 512: CK = 8):
+// each lane keeps its CK channels' weights, biases and values in registers
+// and issues a position's CK positional loads together; CK = 0 is the
+// general loop for any c.
+template <int TOK_POS, int NT, int CK>
+__global__ __launch_bounds__(NT) void channels_to_tokens_ln_kernel(const float *__restrict__ x, int B, int c, int F,
+                                                                   int T, const float *__restrict__ w,
+                                                                   const float *__restrict__ bias,
+                                                                   const float *__restrict__ pos, float pos_weight,
+                                                                   float *__restrict__ out) {
     extern __shared__ float tile[];  // [c][TOK_POS + 1]
-    const int P = F * T, b = blockIdx.y, p0 = blockIdx.x * TOK_POS;
+    constexpr int S = TOK_POS + 1, Q = TOK_POS / 4, WAVES = NT / 64;
+    const int P = F * T, NP = (P + TOK_POS - 1) / TOK_POS;
+    const int items = NP * B, per_xcd = (items + TOK_XCDS - 1) / TOK_XCDS;
+    const int item = (int)(blockIdx.x % TOK_XCDS) * per_xcd + (int)(blockIdx.x / TOK_XCDS);
+    if (item >= items || (int)(blockIdx.x / TOK_XCDS) >= per_xcd) return;
+    const int b = item % B, p0 = (item / B) * TOK_POS;
     const float *xb = x + (int64_t)b * c * P;
-    for (int e = threadIdx.x; e < c * TOK_POS; e += 256) {
-        int ch = e / TOK_POS, pi = e % TOK_POS, p = p0 + pi;
-        tile[ch * (TOK_POS + 1) + pi] = p < P ? xb[(int64_t)ch * P + p] : 0.0f;
-    }
-    __syncthreads();
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    for (int pi = wave; pi < TOK_POS; pi += 4) {
-        int p = p0 + pi;
-        if (p >= P) break;
-        float s = 0.0f;
-        for (int ch = lane; ch < c; ch += 64) s += tile[ch * (TOK_POS + 1) + pi];
-        float mean = wave_sum(s) / (float)c;
-        float v = 0.0f;
-        for (int ch = lane; ch < c; ch += 64) {
-            float d = tile[ch * (TOK_POS + 1) + pi] - mean;
-            v += d * d;
+    if ((P & 3) == 0 && p0 + TOK_POS <= P) {
+        for (int e = threadIdx.x; e < c * Q; e += NT) {
+            const int ch = e / Q, q = e - ch * Q;
+            const float4 v = *reinterpret_cast<const float4 *>(xb + (int64_t)ch * P + p0 + 4 * q);
+            float *t = tile + ch * S + 4 * q;
+            t[0] = v.x;
+            t[1] = v.y;
+            t[2] = v.z;
+            t[3] = v.w;
         }
-        float var = wave_sum(v) / (float)c;
-        float inv = 1.0f / sqrtf(var + 1e-5f);
-        int f = p / T, t = p - f * T, token = t * F + f;
-        float *orow = out + ((int64_t)b * P + token) * c;
-        const float *prow = pos ? pos + (int64_t)token * c : nullptr;
-        for (int ch = lane; ch < c; ch += 64) {
-            float y = (tile[ch * (TOK_POS + 1) + pi] - mean) * inv * w[ch] + bias[ch];
-            if (prow) y = y + prow[ch] * pos_weight;
-            orow[ch] = y;
+    } else {
+        for (int e = threadIdx.x; e < c * TOK_POS; e += NT) {
+            const int ch = e / TOK_POS, pi = e - ch * TOK_POS, p = p0 + pi;
+            tile[ch * S + pi] = p < P ? xb[(int64_t)ch * P + p] : 0.0f;
+        }
+    }
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    if constexpr (CK > 0) {
+        float wv[CK], bv[CK];
+#pragma unroll
+        for (int k = 0; k < CK; ++k) {
+            wv[k] = w[lane + 64 * k];
+            bv[k] = bias[lane + 64 * k];
+        }
+        __syncthreads();
+        for (int pi = wave; pi < TOK_POS; pi += WAVES) {
+            const int p = p0 + pi;
+            if (p >= P) break;
+            const int f = p / T, t = p - f * T, token = t * F + f;
+            float pv[CK];
+            const float *prow = pos ? pos + (int64_t)token * c : nullptr;
+#pragma unroll
+            for (int k = 0; k < CK; ++k) pv[k] = prow ? prow[lane + 64 * k] : 0.0f;
+            float xv[CK];
+            float s = 0.0f;
+#pragma unroll
+            for (int k = 0; k < CK; ++k) {
+                xv[k] = tile[(lane + 64 * k) * S + pi];
+                s += xv[k];
+            }
+            const float mean = wave_sum(s) / (float)c;
+            float v = 0.0f;
+#pragma unroll
+            for (int k = 0; k < CK; ++k) {
+                const float d = xv[k] - mean;
+                v += d * d;
+            }
+            const float var = wave_sum(v) / (float)c;
+            const float inv = 1.0f / sqrtf(var + 1e-5f);
+            float *orow = out + ((int64_t)b * P + token) * c;
+#pragma unroll
+            for (int k = 0; k < CK; ++k) {
+                float y = (xv[k] - mean) * inv * wv[k] + bv[k];
+                if (prow) y = y + pv[k] * pos_weight;
+                orow[lane + 64 * k] = y;
+            }
+        }
+    } else {
+        __syncthreads();
+        for (int pi = wave; pi < TOK_POS; pi += WAVES) {
+            const int p = p0 + pi;
+            if (p >= P) break;
+            float s = 0.0f;
+            for (int ch = lane; ch < c; ch += 64) s += tile[ch * S + pi];
+            const float mean = wave_sum(s) / (float)c;
+            float v = 0.0f;
+            for (int ch = lane; ch < c; ch += 64) {
+                const float d = tile[ch * S + pi] - mean;
+                v += d * d;
+            }
+            const float var = wave_sum(v) / (float)c;
+            const float inv = 1.0f / sqrtf(var + 1e-5f);
+            const int f = p / T, t = p - f * T, token = t * F + f;
+            float *orow = out + ((int64_t)b * P + token) * c;
+            const float *prow = pos ? pos + (int64_t)token * c : nullptr;
+            for (int ch = lane; ch < c; ch += 64) {
+                float y = (tile[ch * S + pi] - mean) * inv * w[ch] + bias[ch];
+                if (prow) y = y + prow[ch] * pos_weight;
+                orow[ch] = y;
+            }
         }
     }
 }
@@ -255,15 +325,38 @@ void layer_norm_rows(hipStream_t s, const float *x, int rows, int dim, const flo
     DMX_LAUNCH_CHECK();
 }
 
+template <int TOK_POS, int NT>
+void launch_tokens_ln(hipStream_t s, const float *x, int b, int c, int F, int T, const float *w, const float *bias,
+                      const float *pos, float pos_weight, float *out) {
+    const size_t shmem = (size_t)c * (TOK_POS + 1) * sizeof(float);
+    constexpr size_t LDS_MAX = 96 * 1024;
+    DMX_REQUIRE(shmem <= LDS_MAX, "channels_to_tokens_ln: too many channels");
+    const int64_t items = ceil_div((int64_t)F * T, TOK_POS) * b;
+    const int64_t per_xcd = ceil_div(items, TOK_XCDS);
+    auto go = [&](auto kernel) {
+        static const bool lds_ok = hipFuncSetAttribute(reinterpret_cast<const void *>(kernel),
+                                                       hipFuncAttributeMaxDynamicSharedMemorySize,
+                                                       (int)LDS_MAX) == hipSuccess;
+        DMX_REQUIRE(lds_ok, "channels_to_tokens_ln: the kernel's LDS limit could not be raised");
+        hipLaunchKernelGGL(kernel, dim3((unsigned)(per_xcd * TOK_XCDS)), dim3(NT), shmem, s, x, b, c, F, T, w, bias,
+                           pos, pos_weight, out);
+    };
+    if (c == 512)
+        go(channels_to_tokens_ln_kernel<TOK_POS, NT, 8>);
+    else
+        go(channels_to_tokens_ln_kernel<TOK_POS, NT, 0>);
+    DMX_LAUNCH_CHECK();
+}
+
 void channels_to_tokens_ln(hipStream_t s, const float *x, int b, int c, int F, int T, const float *w,
                            const float *bias, const float *pos, float pos_weight, float *out) {
     require_ptrs({x, w, bias, out}, "channels_to_tokens_ln");
-    size_t shmem = (size_t)c * (TOK_POS + 1) * sizeof(float);
-    DMX_REQUIRE(shmem <= 64 * 1024, "channels_to_tokens_ln: too many channels");
-    dim3 grid((unsigned)ceil_div((int64_t)F * T, TOK_POS), (unsigned)b);
-    hipLaunchKernelGGL(channels_to_tokens_ln_kernel, grid, dim3(256), shmem, s, x, c, F, T, w, bias, pos, pos_weight,
-                       out);
-    DMX_LAUNCH_CHECK();
+    // Eight positions per block: a channel row's run is 32 B (two float4),
+    // the LDS tile 17 KB, and every wave writes two token rows. Measured at
+    // B = 8, c = 512 (2688 and 1344 tokens): 23 and 13 us; blocks of 16 and
+    // 32 positions took 26 and 34 us, since a block's rows are written one
+    // position per wave after its loads.
+    launch_tokens_ln<8, 256>(s, x, b, c, F, T, w, bias, pos, pos_weight, out);
 }
 
 void group_norm_tokens_apply(hipStream_t s, float *x, int b, int L, int C, const double *stats, const float *w,

@@ -19,6 +19,7 @@
 #include <functional>
 #include <mutex>
 #include <set>
+#include <string>
 #include <thread>
 #include <vector>
 
@@ -65,6 +66,49 @@ void advise_huge_pages(void *p, size_t n);
 // Maps every page of [p, p + n) for writing without changing its contents,
 // on huge pages where the kernel allows them (asynchronous).
 uint64_t prefault_async(void *p, size_t n);
+
+// One host-to-host copy.
+struct Copy {
+    void *dst;
+    const void *src;
+    size_t bytes;
+};
+
+// Every range of `copies` on the pool as one job, split evenly by bytes
+// (asynchronous; wait on the ticket).
+uint64_t host_copy_ranges_async(std::vector<Copy> copies);
+
+// Host copies that wait for device events, run from a thread of its own: the
+// caller queues (event, copies) pairs in order while it goes on enqueueing
+// GPU work, and each pair's copies start on the pool as soon as its event has
+// completed. finish() (also run by the destructor) returns when every queued
+// copy is done and reports the first failure as a dmx::Error. The pool jobs
+// in `before` (e.g. the prefault of the same destination pages) end before
+// the first copy starts.
+class EventCopier {
+  public:
+    EventCopier(int device, std::vector<uint64_t> before);
+    EventCopier(const EventCopier &) = delete;
+    EventCopier &operator=(const EventCopier &) = delete;
+    ~EventCopier();
+    void push(hipEvent_t ev, std::vector<Copy> copies);
+    void finish();
+
+  private:
+    struct Task {
+        hipEvent_t ev;
+        std::vector<Copy> copies;
+    };
+    void run();
+    int device_;
+    std::vector<uint64_t> before_;
+    std::mutex mu_;
+    std::condition_variable cv_;
+    std::deque<Task> tasks_;
+    bool closed_ = false;
+    std::string error_;
+    std::thread thread_;
+};
 
 // One contiguous range moved between host and device memory.
 struct Span {

@@ -17,7 +17,7 @@ namespace {
 constexpr size_t PAGE = 4096;
 constexpr size_t HUGE_PAGE = 2u << 20;
 // Below this a copy is not split: a part costs a wake-up (~10 us).
-constexpr size_t MIN_PART = 1u << 20;
+constexpr size_t MIN_PART = 512u << 10;
 
 int pool_threads() {
     if (const char *v = std::getenv("DMX_HOST_THREADS")) {
@@ -126,6 +126,90 @@ uint64_t prefault_async(void *p, size_t n) {
             }
         },
         parts);
+}
+
+uint64_t host_copy_ranges_async(std::vector<Copy> copies) {
+    HostPool &pool = HostPool::instance();
+    size_t total = 0;
+    for (const Copy &c : copies) total += c.bytes;
+    const int parts = (int)std::max<size_t>(1, std::min<size_t>(pool.threads() + 1, total / MIN_PART));
+    // Part i copies bytes [lo, hi) of the ranges laid end to end.
+    return pool.submit(
+        [copies = std::move(copies), total](int i, int k) {
+            size_t lo, hi;
+            part_range(total, i, k, lo, hi);
+            size_t at = 0;
+            for (const Copy &c : copies) {
+                const size_t a = std::max(lo, at), b = std::min(hi, at + c.bytes);
+                if (b > a)
+                    std::memcpy(static_cast<char *>(c.dst) + (a - at), static_cast<const char *>(c.src) + (a - at),
+                                b - a);
+                at += c.bytes;
+                if (at >= hi) break;
+            }
+        },
+        parts);
+}
+
+EventCopier::EventCopier(int device, std::vector<uint64_t> before)
+    : device_(device), before_(std::move(before)), thread_([this] { run(); }) {}
+
+EventCopier::~EventCopier() {
+    try {
+        finish();
+    } catch (...) {
+    }
+}
+
+void EventCopier::push(hipEvent_t ev, std::vector<Copy> copies) {
+    {
+        std::lock_guard<std::mutex> lock(mu_);
+        tasks_.push_back({ev, std::move(copies)});
+    }
+    cv_.notify_one();
+}
+
+void EventCopier::finish() {
+    {
+        std::lock_guard<std::mutex> lock(mu_);
+        closed_ = true;
+    }
+    cv_.notify_one();
+    if (thread_.joinable()) thread_.join();
+    if (!error_.empty()) {
+        std::string msg;
+        msg.swap(error_);
+        throw_error(6, msg);
+    }
+}
+
+void EventCopier::run() {
+    const bool device_ok = hipSetDevice(device_) == hipSuccess;
+    for (;;) {
+        Task t;
+        {
+            std::unique_lock<std::mutex> lock(mu_);
+            cv_.wait(lock, [this] { return closed_ || !tasks_.empty(); });
+            if (tasks_.empty()) return;
+            t = std::move(tasks_.front());
+            tasks_.pop_front();
+        }
+        // After a failure the rest of the queue is dropped: its host memory
+        // may not hold what the device wrote.
+        if (!error_.empty()) continue;
+        if (!device_ok) {
+            error_ = "readback thread: hipSetDevice(" + std::to_string(device_) + ") failed";
+            continue;
+        }
+        const hipError_t e = hipEventSynchronize(t.ev);
+        if (e != hipSuccess) {
+            error_ = std::string("readback thread: hipEventSynchronize failed: ") + hipGetErrorString(e);
+            continue;
+        }
+        for (uint64_t b : before_) HostPool::instance().wait(b);
+        before_.clear();
+        HostPool::instance().wait(host_copy_ranges_async(std::move(t.copies)));
+    }
 }
 
 PinnedRing::~PinnedRing() {
