@@ -19,7 +19,7 @@ from typing import Callable, Dict, List, Mapping, Optional, Sequence
 
 import numpy as np
 
-from . import _native, signals
+from . import _native, audio, signals
 from .config import Config
 from .checkpoint import LoadedWeights, config_from_kwargs, load_weights, load_weights_from_bytes
 from .weights import random_init, weight_shapes, xavier_transformer_init
@@ -32,7 +32,7 @@ __all__ = [
 
 # dmx_status -> reference Error variant (crates/demucs-core/src/error.rs:4-55)
 STATUS_NAMES = {1: "Shape", 2: "Config", 3: "MissingWeight", 4: "WeightShape", 5: "UnsupportedModel", 6: "Gpu",
-                7: "Memory", 8: "Argument", 9: "Checkpoint", 10: "Io"}
+                7: "Memory", 8: "Argument", 9: "Checkpoint", 10: "Io", 11: "Audio"}
 PRECISION_FP32, PRECISION_BF16 = 0, 1
 
 
@@ -283,6 +283,47 @@ def separate_runners(runners: Sequence[Runner], left: np.ndarray, right: np.ndar
     return out
 
 
+def separate_emit_runners(runners: Sequence[Runner], left: np.ndarray, right: np.ndarray, sample_rate: int,
+                          options: SeparateOptions, on_frames: Callable[[int, np.ndarray], None],
+                          bag_weights: Optional[np.ndarray] = None, wanted: Optional[Sequence[bool]] = None,
+                          on_progress: Optional[Callable[[SeparationProgress], None]] = None) -> None:
+    """dmx_separate_emit: `on_frames(start, stems)` receives each finished
+    region in order as (sources, 2, frames) float32 (rows of unwanted stems
+    are zero), while later chunk groups still compute. An exception raised by
+    `on_frames` stops the separation and propagates."""
+    lib = _native.load()
+    left, right = _f32(left), _f32(right)
+    if left.shape != right.shape:
+        raise DmxError(1, f"left/right lengths differ ({left.shape[0]} vs {right.shape[0]})")
+    sources = runners[0].config.sources
+    handles = (ctypes.c_void_p * len(runners))(*[r.handle for r in runners])
+    w = None if bag_weights is None else _f32(bag_weights).reshape(len(runners), sources)
+    mask = None if wanted is None else np.array([1 if x else 0 for x in wanted], dtype=np.uint8)
+    opts = options.to_c()
+    failure = []
+
+    def _emit(start, frames, rows, _user):
+        try:
+            block = np.zeros((sources, 2, frames), dtype=np.float32)
+            for r in range(2 * sources):
+                if rows[r]:
+                    block[r // 2, r % 2] = np.ctypeslib.as_array(rows[r], shape=(frames,))
+            on_frames(int(start), block)
+            return 0
+        except BaseException as exc:  # handed back after the C call returns
+            failure.append(exc)
+            return 1
+
+    emit_cb = _native.EMIT(_emit)
+    cb = _native.PROGRESS(lambda d, t, _u: on_progress(SeparationProgress(d, t))) if on_progress else _native.PROGRESS()
+    rc = lib.dmx_separate_emit(handles, None if w is None else _ptr(w), len(runners),
+                               None if mask is None else _ptr(mask), _ptr(left), _ptr(right), left.shape[0],
+                               sample_rate, ctypes.byref(opts), cb, None, emit_cb, None)
+    if failure:
+        raise failure[0]
+    _check(rc)
+
+
 class Demucs:
     """`Demucs` (api.rs:374-447): one network or the fine-tuned bag."""
 
@@ -346,3 +387,35 @@ class Demucs:
         wanted = [self.opts.stems.wants(i) for i in ids]
         out = separate_runners(self.runners, left, right, sample_rate, options, self.bag_weights, wanted, on_progress)
         return [Stem(i, out[k, 0].copy(), out[k, 1].copy()) for k, i in enumerate(ids) if wanted[k]]
+
+    def separate_streaming(self, left, right, sample_rate: int, options: SeparateOptions,
+                           on_frames: Callable[[int, np.ndarray], None],
+                           on_progress: Optional[Callable[[SeparationProgress], None]] = None) -> None:
+        """`separate_streaming` (api.rs:617-654) a region at a time: each
+        finished region of denormalised stems goes to `on_frames(start,
+        stems)` in order, stems (sources, 2, frames) with unwanted rows zero,
+        while later chunk groups still compute."""
+        ids = [StemId.parse(n) for n in self.sources]
+        wanted = [self.opts.stems.wants(i) for i in ids]
+        separate_emit_runners(self.runners, left, right, sample_rate, options, on_frames, self.bag_weights, wanted,
+                              on_progress)
+
+    def _read_mix(self, path) -> np.ndarray:
+        from .audio import read_audio
+        a = read_audio(path).ensure_channels(2)
+        if a.sample_rate != self.sample_rate:
+            raise DmxError(1, f"{path} is at {a.sample_rate} Hz but the model wants {self.sample_rate} Hz")
+        return a.data
+
+    def separate_file(self, path, on_progress: Optional[Callable[[SeparationProgress], None]] = None,
+                      options: Optional[SeparateOptions] = None) -> List[Stem]:
+        """`separate_file` (api.rs:786-818): a WAV file (mono duplicated to
+        stereo) at the model's rate; every requested stem."""
+        mix = self._read_mix(path)
+        return self.separate_with_options(mix[0], mix[1], self.sample_rate, options or SeparateOptions(), on_progress)
+
+    def separate_streaming_file(self, path, options: SeparateOptions, on_frames: Callable[[int, np.ndarray], None],
+                                on_progress: Optional[Callable[[SeparationProgress], None]] = None) -> None:
+        """`separate_streaming_file` (api.rs:656-695): separate_streaming of a WAV file."""
+        mix = self._read_mix(path)
+        self.separate_streaming(mix[0], mix[1], self.sample_rate, options, on_frames, on_progress)

@@ -19,6 +19,7 @@ c_uint8_p = ctypes.POINTER(ctypes.c_uint8)
 TRACE_WANTS = ctypes.CFUNCTYPE(ctypes.c_int, ctypes.c_char_p, ctypes.c_void_p)
 TRACE_RECORD = ctypes.CFUNCTYPE(None, ctypes.c_char_p, c_int64_p, ctypes.c_int32, c_float_p, ctypes.c_void_p)
 PROGRESS = ctypes.CFUNCTYPE(None, ctypes.c_size_t, ctypes.c_size_t, ctypes.c_void_p)
+EMIT = ctypes.CFUNCTYPE(ctypes.c_int, ctypes.c_int64, ctypes.c_int64, ctypes.POINTER(c_float_p), ctypes.c_void_p)
 
 
 class CTensor(ctypes.Structure):
@@ -27,6 +28,24 @@ class CTensor(ctypes.Structure):
         ("data", c_float_p),
         ("ndim", ctypes.c_int32),
         ("shape", ctypes.c_int64 * 4),
+    ]
+
+
+class CAudioInfo(ctypes.Structure):
+    _fields_ = [("sample_rate", ctypes.c_int32), ("channels", ctypes.c_int32), ("frames", ctypes.c_int64)]
+
+
+class CComparison(ctypes.Structure):
+    _fields_ = [
+        ("elements", ctypes.c_int64),
+        ("max_abs", ctypes.c_float),
+        ("max_abs_index", ctypes.c_int64),
+        ("max_rel", ctypes.c_float),
+        ("mean_abs", ctypes.c_float),
+        ("reference_max_abs", ctypes.c_float),
+        ("reference_rms", ctypes.c_float),
+        ("rms_relative_error", ctypes.c_float),
+        ("snr_db", ctypes.c_float),
     ]
 
 
@@ -62,6 +81,18 @@ SIGNATURES = {
     "dmx_separate_options_default": (None, [_VP]),
     "dmx_separate": (_I, [_VP, _VP, ctypes.c_int32, _VP, _VP, _VP, _I64, ctypes.c_int32, _VP, PROGRESS, _VP, _VP]),
     "dmx_separate_device": (_I, [_VP, _VP, ctypes.c_int32, _VP, _VP, _I64, ctypes.c_int32, _VP, PROGRESS, _VP, _VP]),
+    "dmx_separate_emit": (_I, [_VP, _VP, ctypes.c_int32, _VP, _VP, _VP, _I64, ctypes.c_int32, _VP, PROGRESS, _VP,
+                               EMIT, _VP]),
+    # include/dmx_audio.h
+    "dmx_audio_probe": (_I, [ctypes.c_char_p, ctypes.POINTER(CAudioInfo)]),
+    "dmx_audio_read": (_I, [ctypes.c_char_p, _VP, _I64, ctypes.POINTER(CAudioInfo)]),
+    "dmx_wav_write": (_I, [ctypes.c_char_p, _I, ctypes.c_int32, ctypes.c_int32, _VP, _I64]),
+    "dmx_wav_writer_create": (_I, [ctypes.c_char_p, ctypes.c_int32, ctypes.c_int32, ctypes.POINTER(_VP)]),
+    "dmx_wav_writer_write": (_I, [_VP, _VP, _I64]),
+    "dmx_wav_writer_write_planar": (_I, [_VP, _VP, _I64, _I64]),
+    "dmx_wav_writer_frames": (_I64, [_VP]),
+    "dmx_wav_writer_finish": (_I, [_VP]),
+    "dmx_compare": (_I, [_VP, _VP, _I64, ctypes.POINTER(CComparison)]),
     # include/dmx_ops.h
     "dmx_op_conv2d": (_I, [_VP, _VP, _VP] + [_I] * 4 + [_VP, _VP] + [_I] * 10 + [_VP]),
     "dmx_op_conv2d_glu": (_I, [_VP, _VP, _VP] + [_I] * 4 + [_VP, _VP] + [_I] * 5 + [_VP, _F, _VP]),

@@ -8,15 +8,9 @@
 #include <stdexcept>
 #include <string>
 
+#include "status.h"
+
 namespace dmx {
-
-// Error carrying one of the dmx_status codes of include/dmx.h.
-struct Error : std::runtime_error {
-    int code;
-    Error(int c, const std::string &msg) : std::runtime_error(msg), code(c) {}
-};
-
-[[noreturn]] inline void throw_error(int code, const std::string &msg) { throw Error(code, msg); }
 
 #define DMX_HIP(expr)                                                                             \
     do {                                                                                          \
@@ -42,8 +36,6 @@ inline void require_ptrs(std::initializer_list<const void *> ptrs, const char *w
         if (!p) throw Error(8, std::string(what) + ": null device pointer");
 }
 
-// The calling thread's last error message (dmx_last_error).
-std::string &last_error_slot();
 
 // Input precision of the MFMA contractions (GEMMs, attention) that the
 // calling thread launches. The runner sets it per call from its precision;
@@ -60,25 +52,6 @@ struct MfmaPrecisionScope {
     MfmaPrecisionScope(const MfmaPrecisionScope &) = delete;
     MfmaPrecisionScope &operator=(const MfmaPrecisionScope &) = delete;
 };
-
-// Runs f, turning exceptions into a dmx_status code and a message.
-template <class F>
-int guarded(F &&f) {
-    try {
-        f();
-        last_error_slot().clear();
-        return 0;
-    } catch (const Error &e) {
-        last_error_slot() = e.what();
-        return e.code;
-    } catch (const std::bad_alloc &) {
-        last_error_slot() = "out of host memory";
-        return 7;
-    } catch (const std::exception &e) {
-        last_error_slot() = e.what();
-        return 6;
-    }
-}
 
 // ---------------------------------------------------------------------------
 // Device math shared by every kernel.

@@ -1302,6 +1302,202 @@ std::string &last_error_slot() {
 }
 }  // namespace dmx
 
+namespace dmx {
+namespace {
+
+// dmx_separate and dmx_separate_emit: the mix goes up through the runner's
+// pinned staging, the chunk loop runs on the device, and each finished
+// region of the stems comes back into pinned memory while later groups
+// compute (the OlaRing flush after each segment, streaming.rs:96-261,
+// :389-394). Then either a thread of the call copies each region into
+// `stems_out` as soon as its readback lands, or the calling thread hands
+// each region to `emit` in order.
+int host_separation(dmx_runner *const *nets, const float *bag_weights, int32_t n_nets, const uint8_t *stems_wanted,
+                    const float *left, const float *right, int64_t samples, int32_t sample_rate,
+                    const dmx_separate_options *opts, dmx_progress_fn progress, void *user, float *stems_out,
+                    dmx_emit_fn emit, void *emit_user) {
+    std::vector<uint64_t> host_jobs;  // pool jobs that touch the caller's memory
+    int rc = guarded([&] {
+        if (!nets || !nets[0] || !left || !right) throw_error(DMX_ERR_ARGUMENT, "null argument");
+        if (samples <= 0) throw_error(DMX_ERR_SHAPE, "empty mix");
+        dmx_separate_options o;
+        dmx_separate_options_default(&o);
+        if (opts) o = *opts;
+        dmx_runner &r = *nets[0];
+        set_device(&r);
+        hipStream_t s = r.stream;
+        const int S = r.cfg.sources;
+        // Runs of consecutive wanted stems: one 2-D copy each.
+        std::vector<std::pair<int, int>> runs;
+        for (int i = 0; i < S; ++i) {
+            if (stems_wanted && !stems_wanted[i]) continue;
+            if (!runs.empty() && runs.back().first + runs.back().second == i)
+                ++runs.back().second;
+            else
+                runs.push_back({i, 1});
+        }
+        const size_t row_bytes = (size_t)samples * sizeof(float);
+        const size_t need = (size_t)(2 + 2 * S) * row_bytes;
+        const bool staged = need <= pinned_limit();
+        DBuf mix = fbuf(s, 2 * samples), stems = fbuf(s, (int64_t)S * 2 * samples);
+        try {
+            float *pin_mix = nullptr, *pin_stems = nullptr;
+            if (staged) {
+                // Everything on the runner's main stream, in order: the mix
+                // goes up piece by piece (a piece's host copy overlaps the
+                // previous piece's DMA), and each group's finished samples
+                // come back into pinned memory as soon as they are final.
+                pin_mix = reinterpret_cast<float *>(r.staging.reserve(need));
+                pin_stems = pin_mix + 2 * samples;
+                const int64_t piece = 1 << 20;
+                const float *src[2] = {left, right};
+                for (int ch = 0; ch < 2; ++ch)
+                    for (int64_t off = 0; off < samples; off += piece) {
+                        const int64_t n = std::min(piece, samples - off);
+                        float *p = pin_mix + ch * samples + off;
+                        host_copy(p, src[ch] + off, (size_t)n * sizeof(float));
+                        DMX_HIP(hipMemcpyAsync(mix.f() + ch * samples + off, p, (size_t)n * sizeof(float),
+                                               hipMemcpyHostToDevice, s));
+                    }
+            } else {
+                r.ring.upload({{mix.f(), const_cast<float *>(left), row_bytes},
+                               {mix.f() + samples, const_cast<float *>(right), row_bytes}},
+                              s);
+            }
+            // Map the caller's output pages on the host threads while the GPU
+            // works (queued after the upload's copies; the pool runs jobs in
+            // order).
+            if (stems_out)
+                for (const auto &run : runs)
+                    host_jobs.push_back(prefault_async(stems_out + (int64_t)run.first * 2 * samples,
+                                                       (size_t)run.second * 2 * row_bytes));
+            // Each finished region goes back in up to three blocks (at least
+            // 4 MB each): a block's host copy overlaps the next block's DMA,
+            // and every block costs one more gap between DMA commands. With
+            // `stems_out`, a thread of the call waits for each block and runs
+            // its host copies, so they start while this thread is still
+            // enqueueing.
+            EventCopier copier(r.device, host_jobs);
+            struct Block {
+                hipEvent_t ev;
+                int64_t lo, hi;
+            };
+            std::vector<Block> blocks;
+            const int64_t wanted_rows = [&] {
+                int64_t n = 0;
+                for (const auto &run : runs) n += 2 * run.second;
+                return std::max<int64_t>(n, 1);
+            }();
+            auto on_final = [&](int64_t lo, int64_t hi) {
+                const int64_t min_block = std::max<int64_t>(1 << 14, (int64_t)(4u << 20) / (wanted_rows * 4));
+                const int64_t nb = std::max<int64_t>(1, std::min<int64_t>(3, (hi - lo) / min_block));
+                for (int64_t i = 0; i < nb; ++i) {
+                    const int64_t a = lo + (hi - lo) * i / nb, b = lo + (hi - lo) * (i + 1) / nb;
+                    std::vector<Copy> copies;
+                    for (const auto &run : runs) {
+                        const int64_t at = (int64_t)run.first * 2 * samples + a;
+                        DMX_HIP(hipMemcpy2DAsync(pin_stems + at, row_bytes, stems.f() + at, row_bytes,
+                                                 (size_t)(b - a) * sizeof(float), (size_t)run.second * 2,
+                                                 hipMemcpyDeviceToHost, s));
+                        if (stems_out)
+                            for (int row = 0; row < 2 * run.second; ++row)
+                                copies.push_back({stems_out + at + (int64_t)row * samples,
+                                                  pin_stems + at + (int64_t)row * samples,
+                                                  (size_t)(b - a) * sizeof(float)});
+                    }
+                    Block bl{xfer_event(r, blocks.size()), a, b};
+                    DMX_HIP(hipEventRecord(bl.ev, s));
+                    blocks.push_back(bl);
+                    if (stems_out) copier.push(bl.ev, std::move(copies));
+                }
+            };
+            // Rows handed to `emit`: wanted stems' rows, null for the others.
+            std::vector<const float *> rows(2 * S, nullptr);
+            auto emit_rows = [&](const float *base, int64_t row_stride, int64_t lo, int64_t hi) {
+                for (const auto &run : runs)
+                    for (int row = 2 * run.first; row < 2 * (run.first + run.second); ++row)
+                        rows[row] = base + (int64_t)row * row_stride;
+                if (emit(lo, hi - lo, rows.data(), emit_user) != 0)
+                    throw_error(DMX_ERR_IO, "the emit callback stopped the separation at sample " + std::to_string(lo));
+            };
+            std::vector<GroupMark> marks;
+            size_t total = 0;
+            try {
+                // The second lane's group starts after the first group's
+                // third transformer layer: the first group then ends early
+                // enough for its readback (66 MB of a 60 s mix's 85 MB of
+                // stems) to overlap the second group's work. Against the
+                // start at the transformer (dmx_separate_device's) the
+                // forwards take 1.3 % longer and the call 3.5 % less time.
+                if (staged)
+                    separate_device(nets, bag_weights, n_nets, stems_wanted, mix.f(), samples, sample_rate, o,
+                                    stems.f(), marks, total, 32, on_final);
+                else
+                    separate_device(nets, bag_weights, n_nets, stems_wanted, mix.f(), samples, sample_rate, o,
+                                    stems.f(), marks, total);
+                // Progress after each group, and (emit) each readback block
+                // once it has landed, in order, on this thread.
+                size_t bi = 0;
+                for (const GroupMark &m : marks) {
+                    if (emit)
+                        for (; bi < blocks.size() && blocks[bi].hi <= m.hi; ++bi) {
+                            DMX_HIP(hipEventSynchronize(blocks[bi].ev));
+                            emit_rows(pin_stems + blocks[bi].lo, samples, blocks[bi].lo, blocks[bi].hi);
+                        }
+                    if (progress) {
+                        DMX_HIP(hipEventSynchronize(m.ev));
+                        progress(m.done, total, user);
+                    }
+                }
+            } catch (...) {
+                // No host copy may outlive the call that owns its destination.
+                for (hipStream_t st : {r.stream, r.side, r.stream_b, r.side_b}) (void)hipStreamSynchronize(st);
+                try {
+                    copier.finish();
+                } catch (...) {
+                }
+                throw;
+            }
+            copier.finish();
+            if (!staged) {
+                if (stems_out) {
+                    std::vector<Span> spans;
+                    for (const auto &run : runs) {
+                        const int64_t at = (int64_t)run.first * 2 * samples;
+                        spans.push_back({stems.f() + at, stems_out + at, (size_t)run.second * 2 * row_bytes});
+                    }
+                    r.ring.download(spans, s);
+                } else {
+                    // Too long for the pinned staging: the regions go out
+                    // after the chunk loop, a block of rows at a time.
+                    DMX_HIP(hipStreamSynchronize(s));
+                    const int64_t block = std::max<int64_t>(1 << 14, (int64_t)(8u << 20) / (wanted_rows * 4));
+                    std::vector<float> host((size_t)(2 * S) * (size_t)std::min(block, samples));
+                    for (int64_t lo = 0; lo < samples; lo += block) {
+                        const int64_t n = std::min(block, samples - lo);
+                        for (const auto &run : runs)
+                            DMX_HIP(hipMemcpy2D(host.data() + (size_t)(2 * run.first) * n, (size_t)n * sizeof(float),
+                                                stems.f() + (int64_t)run.first * 2 * samples + lo, row_bytes,
+                                                (size_t)n * sizeof(float), (size_t)run.second * 2,
+                                                hipMemcpyDeviceToHost));
+                        emit_rows(host.data(), n, lo, lo + n);
+                    }
+                }
+            }
+            DMX_HIP(hipStreamSynchronize(s));
+        } catch (...) {
+            // The device buffers go back to the pool: let nothing use them.
+            for (hipStream_t st : {r.stream, r.side, r.stream_b, r.side_b}) (void)hipStreamSynchronize(st);
+            throw;
+        }
+    });
+    for (uint64_t t : host_jobs) HostPool::instance().wait(t);
+    return rc;
+}
+
+}  // namespace
+}  // namespace dmx
+
 using namespace dmx;
 
 extern "C" {
@@ -1579,139 +1775,18 @@ int dmx_separate_device(dmx_runner *const *nets, const float *bag_weights, int32
 int dmx_separate(dmx_runner *const *nets, const float *bag_weights, int32_t n_nets, const uint8_t *stems_wanted,
                  const float *left, const float *right, int64_t samples, int32_t sample_rate,
                  const dmx_separate_options *opts, dmx_progress_fn progress, void *user, float *stems_out) {
-    std::vector<uint64_t> host_jobs;  // pool jobs that touch the caller's memory
-    int rc = guarded([&] {
-        if (!nets || !nets[0] || !left || !right || !stems_out) throw_error(DMX_ERR_ARGUMENT, "null argument");
-        if (samples <= 0) throw_error(DMX_ERR_SHAPE, "empty mix");
-        dmx_separate_options o;
-        dmx_separate_options_default(&o);
-        if (opts) o = *opts;
-        dmx_runner &r = *nets[0];
-        set_device(&r);
-        hipStream_t s = r.stream;
-        const int S = r.cfg.sources;
-        // Runs of consecutive wanted stems: one 2-D copy each.
-        std::vector<std::pair<int, int>> runs;
-        for (int i = 0; i < S; ++i) {
-            if (stems_wanted && !stems_wanted[i]) continue;
-            if (!runs.empty() && runs.back().first + runs.back().second == i)
-                ++runs.back().second;
-            else
-                runs.push_back({i, 1});
-        }
-        const size_t row_bytes = (size_t)samples * sizeof(float);
-        const size_t need = (size_t)(2 + 2 * S) * row_bytes;
-        const bool staged = need <= pinned_limit();
-        DBuf mix = fbuf(s, 2 * samples), stems = fbuf(s, (int64_t)S * 2 * samples);
-        try {
-            float *pin_mix = nullptr, *pin_stems = nullptr;
-            if (staged) {
-                // Everything on the runner's main stream, in order: the mix
-                // goes up piece by piece (a piece's host copy overlaps the
-                // previous piece's DMA), and each group's finished samples
-                // come back into pinned memory as soon as they are final.
-                pin_mix = reinterpret_cast<float *>(r.staging.reserve(need));
-                pin_stems = pin_mix + 2 * samples;
-                const int64_t piece = 1 << 20;
-                const float *src[2] = {left, right};
-                for (int ch = 0; ch < 2; ++ch)
-                    for (int64_t off = 0; off < samples; off += piece) {
-                        const int64_t n = std::min(piece, samples - off);
-                        float *p = pin_mix + ch * samples + off;
-                        host_copy(p, src[ch] + off, (size_t)n * sizeof(float));
-                        DMX_HIP(hipMemcpyAsync(mix.f() + ch * samples + off, p, (size_t)n * sizeof(float),
-                                               hipMemcpyHostToDevice, s));
-                    }
-            } else {
-                r.ring.upload({{mix.f(), const_cast<float *>(left), row_bytes},
-                               {mix.f() + samples, const_cast<float *>(right), row_bytes}},
-                              s);
-            }
-            // Map the caller's output pages on the host threads while the GPU
-            // works (queued after the upload's copies; the pool runs jobs in
-            // order).
-            for (const auto &run : runs)
-                host_jobs.push_back(prefault_async(stems_out + (int64_t)run.first * 2 * samples,
-                                                   (size_t)run.second * 2 * row_bytes));
-            // Each finished region goes back in up to three blocks (at least
-            // 4 MB each): a block's host copy overlaps the next block's DMA,
-            // and every block costs one more gap between DMA commands. A
-            // thread of the call waits for each block and runs its host
-            // copies, so they start while this thread is still enqueueing.
-            EventCopier copier(r.device, host_jobs);
-            size_t n_blocks = 0;
-            const int64_t wanted_rows = [&] {
-                int64_t n = 0;
-                for (const auto &run : runs) n += 2 * run.second;
-                return std::max<int64_t>(n, 1);
-            }();
-            auto on_final = [&](int64_t lo, int64_t hi) {
-                const int64_t min_block = std::max<int64_t>(1 << 14, (int64_t)(4u << 20) / (wanted_rows * 4));
-                const int64_t nb = std::max<int64_t>(1, std::min<int64_t>(3, (hi - lo) / min_block));
-                for (int64_t i = 0; i < nb; ++i) {
-                    const int64_t a = lo + (hi - lo) * i / nb, b = lo + (hi - lo) * (i + 1) / nb;
-                    std::vector<Copy> copies;
-                    for (const auto &run : runs) {
-                        const int64_t at = (int64_t)run.first * 2 * samples + a;
-                        DMX_HIP(hipMemcpy2DAsync(pin_stems + at, row_bytes, stems.f() + at, row_bytes,
-                                                 (size_t)(b - a) * sizeof(float), (size_t)run.second * 2,
-                                                 hipMemcpyDeviceToHost, s));
-                        for (int row = 0; row < 2 * run.second; ++row)
-                            copies.push_back({stems_out + at + (int64_t)row * samples, pin_stems + at + (int64_t)row * samples,
-                                              (size_t)(b - a) * sizeof(float)});
-                    }
-                    hipEvent_t ev = xfer_event(r, n_blocks++);
-                    DMX_HIP(hipEventRecord(ev, s));
-                    copier.push(ev, std::move(copies));
-                }
-            };
-            std::vector<GroupMark> marks;
-            size_t total = 0;
-            try {
-                // The second lane's group starts after the first group's
-                // third transformer layer: the first group then ends early
-                // enough for its readback (66 MB of a 60 s mix's 85 MB of
-                // stems) to overlap the second group's work. Against the
-                // start at the transformer (dmx_separate_device's) the
-                // forwards take 1.3 % longer and the call 3.5 % less time.
-                if (staged)
-                    separate_device(nets, bag_weights, n_nets, stems_wanted, mix.f(), samples, sample_rate, o,
-                                    stems.f(), marks, total, 32, on_final);
-                else
-                    separate_device(nets, bag_weights, n_nets, stems_wanted, mix.f(), samples, sample_rate, o,
-                                    stems.f(), marks, total);
-                if (progress)
-                    for (const GroupMark &m : marks) {
-                        DMX_HIP(hipEventSynchronize(m.ev));
-                        progress(m.done, total, user);
-                    }
-            } catch (...) {
-                // No host copy may outlive the call that owns its destination.
-                for (hipStream_t st : {r.stream, r.side, r.stream_b, r.side_b}) (void)hipStreamSynchronize(st);
-                try {
-                    copier.finish();
-                } catch (...) {
-                }
-                throw;
-            }
-            copier.finish();
-            if (!staged) {
-                std::vector<Span> spans;
-                for (const auto &run : runs) {
-                    const int64_t at = (int64_t)run.first * 2 * samples;
-                    spans.push_back({stems.f() + at, stems_out + at, (size_t)run.second * 2 * row_bytes});
-                }
-                r.ring.download(spans, s);
-            }
-            DMX_HIP(hipStreamSynchronize(s));
-        } catch (...) {
-            // The device buffers go back to the pool: let nothing use them.
-            for (hipStream_t st : {r.stream, r.side, r.stream_b, r.side_b}) (void)hipStreamSynchronize(st);
-            throw;
-        }
-    });
-    for (uint64_t t : host_jobs) HostPool::instance().wait(t);
-    return rc;
+    if (!stems_out) return guarded([] { throw_error(DMX_ERR_ARGUMENT, "null argument"); });
+    return host_separation(nets, bag_weights, n_nets, stems_wanted, left, right, samples, sample_rate, opts, progress,
+                           user, stems_out, nullptr, nullptr);
+}
+
+int dmx_separate_emit(dmx_runner *const *nets, const float *bag_weights, int32_t n_nets, const uint8_t *stems_wanted,
+                      const float *left, const float *right, int64_t samples, int32_t sample_rate,
+                      const dmx_separate_options *opts, dmx_progress_fn progress, void *user, dmx_emit_fn emit,
+                      void *emit_user) {
+    if (!emit) return guarded([] { throw_error(DMX_ERR_ARGUMENT, "null emit callback"); });
+    return host_separation(nets, bag_weights, n_nets, stems_wanted, left, right, samples, sample_rate, opts, progress,
+                           user, nullptr, emit, emit_user);
 }
 
 }  // extern "C"

@@ -36,7 +36,8 @@ enum dmx_status {
     DMX_ERR_MEMORY = 7,         /* Error::Memory */
     DMX_ERR_ARGUMENT = 8,       /* null pointer / bad enum at the C boundary */
     DMX_ERR_CHECKPOINT = 9,     /* Error::Checkpoint / Error::Pickle (dmx_ckpt.h) */
-    DMX_ERR_IO = 10             /* Error::Io (dmx_ckpt.h) */
+    DMX_ERR_IO = 10,            /* Error::Io (dmx_ckpt.h, dmx_audio.h) */
+    DMX_ERR_AUDIO = 11          /* Error::Audio (dmx_audio.h) */
 };
 
 enum dmx_precision {
@@ -175,6 +176,23 @@ int dmx_separate(dmx_runner *const *nets, const float *bag_weights, int32_t n_ne
                  const uint8_t *stems_wanted, const float *left, const float *right,
                  int64_t samples, int32_t sample_rate, const dmx_separate_options *opts,
                  dmx_progress_fn progress, void *user, float *stems_out);
+
+/* The stems of output samples [start, start + frames), handed over in
+ * order: rows[2 * s + c] points at `frames` samples of stem s, channel c
+ * (NULL for a stem not wanted). The memory is the runner's and is valid
+ * only during the call. Return 0 to go on; anything else stops the
+ * separation, which then returns DMX_ERR_IO. */
+typedef int (*dmx_emit_fn)(int64_t start, int64_t frames, const float *const *rows, void *user);
+/* Separate::separate_emit / separate_streaming_normalized_mix
+ * (crates/demucs-core/src/api.rs:265-298, :697-785): dmx_separate, but
+ * instead of filling a (sources, 2, samples) host array it hands each
+ * finished region to `emit` on the calling thread as soon as its readback
+ * has landed (the reference's on_frame, a region at a time), while later
+ * chunk groups still compute. Denormalised, like dmx_separate's stems. */
+int dmx_separate_emit(dmx_runner *const *nets, const float *bag_weights, int32_t n_nets,
+                      const uint8_t *stems_wanted, const float *left, const float *right,
+                      int64_t samples, int32_t sample_rate, const dmx_separate_options *opts,
+                      dmx_progress_fn progress, void *user, dmx_emit_fn emit, void *emit_user);
 /* Same with device-resident mix (2, samples) and stems (sources, 2, samples),
  * enqueued on the runner's stream; without a progress callback it returns
  * before the GPU has finished. */

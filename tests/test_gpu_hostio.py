@@ -140,3 +140,58 @@ def test_collect_rejects_another_runners_group(dmx, small):
         other.collect(p)
     assert e.value.kind == "Argument"
     runner.collect(p)
+
+
+@pytest.mark.parametrize("seconds,shifts,group,pinned_mb", [(2.05, 1, 3, None), (1.7, 2, 2, None),
+                                                            (1.3, 0, 2, "0")])
+def test_emit_hands_over_the_separation_region_by_region(dmx, small, monkeypatch, seconds, shifts, group,
+                                                         pinned_mb):
+    """dmx_separate_emit (separate_emit / separate_streaming_normalized_mix,
+    crates/demucs-core/src/api.rs:265-298, :697-785): the regions come in
+    order, tile [0, samples) exactly, and hold dmx_separate's stems; rows of
+    unwanted stems are null. pinned_mb = 0 takes the path for mixes longer
+    than the pinned staging (regions after the chunk loop)."""
+    if pinned_mb is not None:
+        monkeypatch.setenv("DMX_PINNED_MAX_MB", pinned_mb)
+    cfg, runner = small
+    mix = dmx.signals.synthetic_mix(5, seconds)
+    opts = dmx.SeparateOptions(shifts=shifts, overlap=0.25, batch_chunks=group)
+    wanted = [True, False, True, True]
+    ref = np.zeros((4, 2, mix.shape[1]), np.float32)
+    separate_host(dmx, [runner], mix, opts, ref, wanted=wanted)
+    got = np.full((4, 2, mix.shape[1]), np.nan, np.float32)
+    regions = []
+    progress = []
+
+    def on_frames(start, block):
+        regions.append((start, block.shape[-1]))
+        got[:, :, start:start + block.shape[-1]] = block
+
+    dmx.separate_emit_runners([runner], mix[0], mix[1], 44100, opts, on_frames, wanted=wanted,
+                              on_progress=lambda p: progress.append((p.done, p.total)))
+    assert regions[0][0] == 0 and sum(n for _, n in regions) == mix.shape[1]
+    assert all(a + n == b for (a, n), (b, _) in zip(regions, regions[1:]))
+    if pinned_mb is None:
+        assert len(regions) >= 2  # regions flushed while later groups computed
+    assert not got[1].any()  # the unwanted stem's rows come as zeros
+    for s in (0, 2, 3):
+        assert snr_db(ref[s], got[s]) > 120.0, s
+    assert progress and progress[-1][0] == progress[-1][1]
+
+
+def test_emit_callback_error_stops_the_separation(dmx, small):
+    cfg, runner = small
+    mix = dmx.signals.synthetic_mix(6, 2.05)
+    opts = dmx.SeparateOptions(shifts=0, overlap=0.25, batch_chunks=2)
+    calls = []
+
+    def on_frames(start, block):
+        calls.append(start)
+        raise KeyError("disk full")
+
+    with pytest.raises(KeyError):
+        dmx.separate_emit_runners([runner], mix[0], mix[1], 44100, opts, on_frames)
+    assert len(calls) == 1
+    # the runner is usable afterwards
+    out = dmx.separate_runners([runner], mix[0], mix[1], 44100, opts)
+    assert np.isfinite(out).all()
