@@ -163,8 +163,10 @@ int dmx_op_dconv_layer(void *stream, float *x, int B, int C, int F, int T, int d
             st((size_t)4 * B * F * sizeof(double));
         std::unique_ptr<Scratch> keep;
         const float *w1g = gemm_weights(s, w1, hidden, C, 1, 3, keep);
+        Scratch gram((size_t)dconv_gram_doubles(hidden) * sizeof(double));
+        dconv_gram_weights(s, w2, b2, C, hidden, static_cast<double *>(gram.p));
         dconv_layer(s, x, B, C, F, T, dilation, w1, w1g, nullptr, b1, hidden, n1w, n1b, w2, b2, n2w, n2b, gamma,
-                    static_cast<float *>(h.p), static_cast<double *>(st.p));
+                    static_cast<const double *>(gram.p), static_cast<float *>(h.p), static_cast<double *>(st.p));
         DMX_HIP(hipStreamSynchronize(s));
     });
 }
@@ -195,8 +197,11 @@ int dmx_op_dconv(void *stream, float *x, int B, int C, int F, int T, int hidden,
                 const float *const *p = params + 9 * d;
                 std::unique_ptr<Scratch> keep;
                 const float *w1g = gemm_weights(s, p[0], hidden, C, 1, 3, keep);
+                Scratch gram((size_t)dconv_gram_doubles(hidden) * sizeof(double));
+                dconv_gram_weights(s, p[4], p[5], C, hidden, static_cast<double *>(gram.p));
                 dconv_layer(s, x, B, C, F, T, 1 << d, p[0], w1g, L[d].w1_t, p[1], hidden, p[2], p[3], p[4], p[5],
-                            p[6], p[7], p[8], static_cast<float *>(h.p), static_cast<double *>(st.p));
+                            p[6], p[7], p[8], static_cast<const double *>(gram.p), static_cast<float *>(h.p),
+                            static_cast<double *>(st.p));
                 DMX_HIP(hipStreamSynchronize(s));
             }
         }

@@ -157,6 +157,47 @@ struct NormGeluQuads {
     }
 };
 
+// Rows of the DConv hidden activation g = GELU(GN1(y)) along t, k-major, for
+// the Gram matrix G = g g^T: batch z is (row z / chunks, t-chunk z % chunks)
+// of `chunk` positions; logical row H is a row of ones (its products give
+// the per-channel sums of g), rows past it and positions past T read zero.
+struct GramRows {
+    static constexpr bool kmajor = true;
+    const float *y;
+    const double *stats;
+    const float *nw, *nb;
+    int H, T, chunk, chunks;
+    struct State {
+        const float *row;  // first position of the chunk, or null for the ones row
+        float scale, shift;
+        int valid;         // positions of this chunk inside the row
+        bool ones;
+    };
+    __device__ bool fast() const { return false; }
+    __device__ State setup(int z, int r) const {
+        const int row = z / chunks, t0 = (z - row * chunks) * chunk;
+        const int valid = min(chunk, T - t0);
+        if (r >= H) return {nullptr, 0.f, 0.f, r == H ? valid : 0, true};
+        float mean, inv;
+        gn_stats(stats + 2 * row, (double)H * (double)T, mean, inv);
+        const float sc = inv * nw[r];
+        return {y + ((int64_t)row * H + r) * T + t0, sc, nb[r] - mean * sc, valid, false};
+    }
+    __device__ float one(const State &s, int k) const {
+        if (k >= s.valid) return 0.f;
+        return s.ones ? 1.f : gelu(s.row[k] * s.scale + s.shift);
+    }
+    __device__ float4 load4_full(const State &st, int k) const { return load4(st, k, 0); }
+    __device__ float4 load4(const State &st, int k, int) const {
+        if (!st.ones && k + 3 < st.valid && ((reinterpret_cast<uintptr_t>(st.row + k) & 15) == 0)) {
+            const float4 v = *reinterpret_cast<const float4 *>(st.row + k);
+            return make_float4(gelu(v.x * st.scale + st.shift), gelu(v.y * st.scale + st.shift),
+                               gelu(v.z * st.scale + st.shift), gelu(v.w * st.scale + st.shift));
+        }
+        return make_float4(one(st, k), one(st, k + 1), one(st, k + 2), one(st, k + 3));
+    }
+};
+
 // Transposed convolution (kernel = 2 * stride) along one axis, every output
 // phase in one GEMM: B[k][n] with k = 2 c + j (input channel c, tap j) and
 // column n = qi * P + t is x[b][c][q - j][t] with q = q0 + qi, zero outside
@@ -476,6 +517,42 @@ struct EpConv2Stats {
             }
     }
     __device__ void finalize(int z) { acc.flush(stats + 2 * z); }
+};
+
+// DConv conv2's GroupNorm moments from the Gram matrix of its input (as the
+// row kernel takes them), instead of a pass that computes conv2 for them:
+// with y = W2 g + b2 over the row's T positions, S = sum_t g and G =
+// sum_t g g^T,
+//   sum y   = V . S + T sum(b2),                  V = sum_o w2[o]
+//   sum y^2 = sum_mn P_mn G_mn + 2 U . S + T sum(b2^2),
+//             P = W2^T W2, U = W2^T b2.
+// `gram` holds P (H x H), U, V and (sum b2, sum b2^2) in f64 (dconv_gram_
+// weights). The GEMM's rows 0..H-1 give G and row H (ones) gives S; each
+// t-chunk of a row adds its share to the row's moments.
+struct EpGramMoments {
+    const double *gram;
+    double *stats;
+    int H, T, chunks;
+    double s = 0.0, q = 0.0;
+    __device__ void init(int) {}
+    __device__ void store(int, int m, int n, float v) {
+        const double *P = gram, *U = gram + H * H, *V = U + H;
+        if (m < H) {
+            q += P[m * H + n] * (double)v;
+        } else {
+            s += V[n] * (double)v;
+            q += 2.0 * U[n] * (double)v;
+        }
+    }
+    __device__ void finalize(int z) {
+        const int row = z / chunks;
+        if (z == row * chunks && threadIdx.x == 0) {
+            const double *c = gram + H * H + 2 * H;
+            s += (double)T * c[0];
+            q += (double)T * c[1];
+        }
+        block_moments_atomic(s, q, stats + 2 * row);
+    }
 };
 
 // DConv conv2, second pass: GN -> GLU -> LayerScale -> residual add into x,
@@ -900,10 +977,48 @@ void conv_transpose_axis(hipStream_t s, const float *x, int b, int ic, int A, in
     gemm_auto<false>(s, M, N, K, b, pw, g, ep);
 }
 
+// P = W2^T W2 (H x H), U = W2^T b2, V = sum_o W2[o], then (sum b2,
+// sum b2^2), in f64, for conv2's moments from a Gram matrix (EpGramMoments);
+// w2 is (O, H). One thread per output.
+__global__ void dconv_gram_weights_kernel(const float *__restrict__ w2, const float *__restrict__ b2, int O, int H,
+                                          double *__restrict__ out) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    const int n = H * H + 2 * H + 2;
+    if (i >= n) return;
+    double acc = 0.0;
+    if (i < H * H) {
+        const int m = i / H, k = i - m * H;
+        for (int o = 0; o < O; ++o) acc += (double)w2[(int64_t)o * H + m] * (double)w2[(int64_t)o * H + k];
+    } else if (i < H * H + H) {
+        const int m = i - H * H;
+        for (int o = 0; o < O; ++o) acc += (double)w2[(int64_t)o * H + m] * (double)b2[o];
+    } else if (i < H * H + 2 * H) {
+        const int m = i - H * H - H;
+        for (int o = 0; o < O; ++o) acc += (double)w2[(int64_t)o * H + m];
+    } else {
+        const bool squares = i == n - 1;
+        for (int o = 0; o < O; ++o) acc += squares ? (double)b2[o] * (double)b2[o] : (double)b2[o];
+    }
+    out[i] = acc;
+}
+
+int64_t dconv_gram_doubles(int H) { return (int64_t)H * H + 2 * H + 2; }
+
+void dconv_gram_weights(hipStream_t s, const float *w2, const float *b2, int C, int H, double *out) {
+    require_ptrs({w2, b2, out}, "dconv_gram_weights");
+    const int n = (int)dconv_gram_doubles(H);
+    hipLaunchKernelGGL(dconv_gram_weights_kernel, dim3((unsigned)ceil_div(n, 256)), dim3(256), 0, s, w2, b2, 2 * C, H,
+                       out);
+    DMX_LAUNCH_CHECK();
+}
+
+// Positions per t-chunk of the Gram launch: 8 k-tiles of MFMA work per block.
+constexpr int GRAM_CHUNK = 128;
+
 void dconv_layer(hipStream_t s, float *x, int B, int C, int F, int T, int dil, const float *w1,
                  const float *w1_gemm, const float *w1_t, const float *b1, int H, const float *n1w,
                  const float *n1b, const float *w2, const float *b2, const float *n2w, const float *n2b,
-                 const float *gamma, float *hbuf, double *stats) {
+                 const float *gamma, const double *gram, float *hbuf, double *stats) {
     require_ptrs({x, w1, w1_gemm, b1, n1w, n1b, w2, b2, n2w, n2b, gamma, hbuf, stats}, "dconv_layer");
     const int rows = B * F;
     DMX_REQUIRE(rows <= 65535, "dconv_layer: too many rows for one launch");
@@ -923,11 +1038,26 @@ void dconv_layer(hipStream_t s, float *x, int B, int C, int F, int T, int dil, c
     e1.T = T;
     conv_dispatch<false>(s, H, T, C * 3, rows, kmajor(w1_gemm, C * 3, 0), x, nullptr, (int64_t)C * F * T, T, F, F, 1, T,
                          1, 3, 1, 1, 0, dil, 1, dil, T, e1);
-    // conv2 (1x1 over H) twice: statistics, then GN + GLU + LayerScale + residual.
+    // conv2's GroupNorm moments: from the Gram matrix of its input when the
+    // folded weights are given, else from a pass that computes conv2 for them.
     EpConv2Stats e2;
     e2.bias = b2;
     e2.stats = st2;
     e2.vec = aligned16(b2);
+    const bool by_gram = gram != nullptr && H + 1 <= 64;
+    if (by_gram) {
+        const int chunks = (int)ceil_div(T, GRAM_CHUNK);
+        DMX_REQUIRE((int64_t)rows * chunks <= 65535, "dconv_layer: too many Gram blocks");
+        EpGramMoments eg;
+        eg.gram = gram;
+        eg.stats = st2;
+        eg.H = H;
+        eg.T = T;
+        eg.chunks = chunks;
+        GramRows g{hbuf, st1, n1w, n1b, H, T, GRAM_CHUNK, chunks};
+        launch_gemm<64, 64, 2, false, false>(s, H + 1, H, GRAM_CHUNK, rows * chunks, g, g, eg);
+    }
+    // Then GN + GLU + LayerScale + residual.
     EpConv2Apply e3;
     e3.x = x;
     e3.bias = b2;
@@ -940,11 +1070,11 @@ void dconv_layer(hipStream_t s, float *x, int B, int C, int F, int T, int dil, c
     e3.T = T;
     if (H % 4 == 0) {
         NormGeluQuads ng{hbuf, st1, n1w, n1b, H, T};
-        gemm_auto<false>(s, 2 * C, T, H, rows, kmajor(w2, H, 0), ng, e2);
+        if (!by_gram) gemm_auto<false>(s, 2 * C, T, H, rows, kmajor(w2, H, 0), ng, e2);
         gemm_auto<true>(s, C, T, H, rows, kmajor(w2, H, 0), ng, e3);
     } else {
         NormGeluRows ng{hbuf, st1, n1w, n1b, H, T};
-        gemm_auto<false>(s, 2 * C, T, H, rows, kmajor(w2, H, 0), ng, e2);
+        if (!by_gram) gemm_auto<false>(s, 2 * C, T, H, rows, kmajor(w2, H, 0), ng, e2);
         gemm_auto<true>(s, C, T, H, rows, kmajor(w2, H, 0), ng, e3);
     }
 }

@@ -77,10 +77,16 @@ void conv3x3_glu_winograd(hipStream_t s, const float *x, const float *skip, int 
 // weight, w1_gemm the same in GEMM order (conv_gemm_weights with kh = 1,
 // kw = 3), w1_t (may be null) the (C*3, H) transpose the narrow path reads
 // (dconv_w1_transposed; made on the device when null).
+// `gram` (dconv_gram_doubles(H) doubles from dconv_gram_weights, or null)
+// lets the MFMA path take conv2's GroupNorm moments from the Gram matrix of
+// its input instead of from a pass that computes conv2 for them.
 void dconv_layer(hipStream_t s, float *x, int B, int C, int F, int T, int dil, const float *w1,
                  const float *w1_gemm, const float *w1_t, const float *b1, int H, const float *n1w,
                  const float *n1b, const float *w2, const float *b2, const float *n2w, const float *n2b,
-                 const float *gamma, float *hbuf, double *stats);
+                 const float *gamma, const double *gram, float *hbuf, double *stats);
+int64_t dconv_gram_doubles(int H);
+// W2^T W2, W2^T b2, sum_o W2[o], sum b2, sum b2^2 of conv2 (w2 (2C, H), b2 (2C)).
+void dconv_gram_weights(hipStream_t s, const float *w2, const float *b2, int C, int H, double *out);
 void dconv_w1_transposed(const float *w1, int C, int H, float *w1_t);
 
 // The same layer with direct VALU kernels for hidden widths where MFMA tiles

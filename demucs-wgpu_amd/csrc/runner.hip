@@ -141,6 +141,7 @@ struct DConvW {
     int hidden;
     const float *w1_gemm;  // w1 in GEMM order (conv_gemm_weights)
     const float *w1_t;     // w1 as (C*3, H) for the narrow path (dconv_w1_transposed), or null
+    const double *gram;    // conv2 folded for its moments from a Gram matrix (dconv_gram_weights), or null
 };
 
 struct LayerW {
@@ -389,13 +390,16 @@ void run_dconv(dmx_runner &r, hipStream_t s, float *x, int B, int C, int F, int 
         }
         if (dconv_rows(s, x, B, C, F, T, L.dconv[0].hidden, rl)) return;
     }
+    // DMX_DCONV_GRAM=0 takes conv2's moments from a conv2 pass instead of
+    // the Gram matrix (tuning).
+    const char *gram_env = std::getenv("DMX_DCONV_GRAM");
+    const bool use_gram = !gram_env || std::atoi(gram_env) != 0;
     for (int d = 0; d < 2; ++d) {
         const DConvW &D = L.dconv[d];
         DBuf h = fbuf(s, dconv_hidden_floats(rows, D.hidden, T));
         DBuf st = dbuf(s, 4 * (int64_t)rows);
         dconv_layer(s, x, B, C, F, T, 1 << d, D.w1, D.w1_gemm, D.w1_t, D.b1, D.hidden, D.n1w, D.n1b, D.w2, D.b2,
-                    D.n2w, D.n2b, D.gamma,
-                    h.f(), st.d());
+                    D.n2w, D.n2b, D.gamma, use_gram ? D.gram : nullptr, h.f(), st.d());
     }
     (void)r;
 }
@@ -934,11 +938,15 @@ void load_weights(dmx_runner &r, const dmx_tensor *weights, size_t n) {
                 dconv_w1_transposed(given[at + ".0.weight"]->data, ch, hid, t.data());
                 w1_t = upload(r, t);
             }
+            double *gram = nullptr;
+            DMX_HIP(hipMalloc((void **)&gram, (size_t)dconv_gram_doubles(hid) * sizeof(double)));
+            r.owned.push_back(gram);
+            dconv_gram_weights(r.stream, dev(r, at + ".3.weight"), dev(r, at + ".3.bias"), ch, hid, gram);
             L.dconv[d] = {dev(r, at + ".0.weight"), dev(r, at + ".0.bias"), dev(r, at + ".1.weight"),
                           dev(r, at + ".1.bias"),   dev(r, at + ".3.weight"), dev(r, at + ".3.bias"),
                           dev(r, at + ".4.weight"), dev(r, at + ".4.bias"), dev(r, at + ".6.scale"),
                           hid,                      gemm_order(at + ".0.weight", hid, ch, 1, 3),
-                          w1_t};
+                          w1_t,                     gram};
         }
     };
     chin = c.audio_channels;
@@ -1573,6 +1581,8 @@ int dmx_runner_create(const dmx_tensor *weights, size_t n_weights, const dmx_con
         DMX_HIP(hipEventCreateWithFlags(&r->ev_lane, hipEventDisableTiming));
         DMX_HIP(hipEventCreateWithFlags(&r->ev_mid, hipEventDisableTiming));
         load_weights(*r, weights, n_weights);
+        // Tables made by kernels at load time are ready before any stream uses them.
+        DMX_HIP(hipStreamSynchronize(r->stream));
     });
     if (rc != DMX_OK) {
         for (hipEvent_t e : {r->ev_fork, r->ev_join, r->ev_lane, r->ev_mid})

@@ -201,7 +201,8 @@ def dconv_reference(oracle, x, w):
 
 
 @pytest.mark.parametrize("B,C,F,T", [(1, 48, 16, 40), (2, 96, 1, 700), (1, 384, 2, 33), (2, 192, 3, 300),
-                                     (1, 48, 1, 1000), (2, 48, 3, 77), (1, 96, 5, 65), (1, 96, 2, 336)])
+                                     (1, 48, 1, 1000), (2, 48, 3, 77), (1, 96, 5, 65), (1, 96, 2, 336),
+                                     (1, 192, 1, 1500), (1, 384, 2, 336)])
 def test_dconv_matches_oracle(lib, oracle, dmx, B, C, F, T):
     hid, w, x = dconv_case(C, C + T, B, F, T)
     ref = dconv_reference(oracle, x, w)
