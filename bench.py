@@ -374,7 +374,7 @@ def profile_workload(pkg, torch, args):
                 raise RuntimeError(pkg._native.last_error())
         what = f"config 5: bf16 forward of {batch} segments (dmx_forward_device)"
     else:
-        runner = pkg.Runner(pkg.random_init(0, cfg), cfg)
+        runner = pkg.Runner(pkg.random_init(0, cfg), cfg, precision=fp32_precision(pkg, args))
         mix = pkg.signals.synthetic_mix(0, args.seconds)
         samples = mix.shape[1]
         opts = pkg.SeparateOptions(shifts=0, overlap=0.25, batch_chunks=args.batch_chunks)
@@ -412,6 +412,11 @@ def profile_workload(pkg, torch, args):
             "ms_per_call": round(ms, 3), "copy_calibration_mib": mib}
 
 
+def fp32_precision(pkg, args):
+    """The runner precision of the fp32 workloads (--precision)."""
+    return pkg.PRECISION_FP32_MFMA if args.precision == "fp32_mfma" else pkg.PRECISION_FP32
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -430,6 +435,9 @@ def main():
                          "host = the config-3 separation from host arrays (dmx_separate), device = the same with "
                          "mix and stems in HBM (dmx_separate_device), bf16 = the config-5 forward of 32 segments; "
                          "each followed by the 256 MiB copy that calibrates the traffic counters")
+    ap.add_argument("--precision", choices=("fp32", "fp32_mfma"), default="fp32",
+                    help="fp32 workloads: fp32 = the default runner precision (transformer linears on three bf16 "
+                         "planes per operand, fp32-accurate); fp32_mfma = fp32 MFMA for every contraction")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py: this build runs on one GPU only; multi-GPU runs are not part of it "
@@ -451,7 +459,7 @@ def main():
         return
     cfg = pkg.Config()
     weights = pkg.random_init(0, cfg)
-    runner = pkg.Runner(weights, cfg, device=0)
+    runner = pkg.Runner(weights, cfg, device=0, precision=fp32_precision(pkg, args))
     mix = pkg.signals.synthetic_mix(0, args.seconds)
     samples = mix.shape[1]
     audio_s = samples / cfg.samplerate

@@ -33,7 +33,9 @@ __all__ = [
 # dmx_status -> reference Error variant (crates/demucs-core/src/error.rs:4-55)
 STATUS_NAMES = {1: "Shape", 2: "Config", 3: "MissingWeight", 4: "WeightShape", 5: "UnsupportedModel", 6: "Gpu",
                 7: "Memory", 8: "Argument", 9: "Checkpoint", 10: "Io", 11: "Audio"}
-PRECISION_FP32, PRECISION_BF16 = 0, 1
+# dmx_precision (include/dmx.h): fp32 results with the transformer linears on
+# three bf16 planes per operand; bf16 MFMA inputs; fp32 MFMA everywhere.
+PRECISION_FP32, PRECISION_BF16, PRECISION_FP32_MFMA = 0, 1, 2
 
 
 class DmxError(RuntimeError):

@@ -98,6 +98,9 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t att_rsrc(const float *base, ui
 struct AttProblem {
     const float *q, *k, *v;
     float *out;
+    unsigned short *out_planes;  // when set: the output as `planes` bf16 planes, plane_stride apart
+    int64_t plane_stride;
+    int planes;
     int64_t ldq, ldk, ldv, ldo, q_bs, kv_bs, o_bs;
     int n_q, n_k, heads, qblocks, blocks;
 };
@@ -124,6 +127,36 @@ __device__ __forceinline__ int att_xcd_block(int bid, const AttProblem &P, bool 
 #endif
 }
 
+// A wave's output rows: lane (query) qi's dims (0|32) + 8 a + 4 half + 0..3
+// from o0/o1 registers 4a..4a+3, times inv, at element offset `at` of the
+// output (fp32, or bf16 planes).
+template <class Acc>
+__device__ __forceinline__ void att_store(const AttProblem &P, int64_t at, int half, const Acc &o0, const Acc &o1,
+                                          float inv) {
+    auto row = [&](int a, int hi) {
+        const Acc &o = hi ? o1 : o0;
+        return make_float4(o[4 * a] * inv, o[4 * a + 1] * inv, o[4 * a + 2] * inv, o[4 * a + 3] * inv);
+    };
+    if (P.out_planes) {
+        unsigned short *prow = P.out_planes + at;
+#pragma unroll
+        for (int a = 0; a < 4; ++a)
+#pragma unroll
+            for (int hi = 0; hi < 2; ++hi) {
+                if (P.planes == 3)
+                    store_planes4<3>(prow + 32 * hi + 8 * a + 4 * half, P.plane_stride, row(a, hi));
+                else
+                    store_planes4<1>(prow + 32 * hi + 8 * a + 4 * half, P.plane_stride, row(a, hi));
+            }
+        return;
+    }
+    float *orow = P.out + at;
+#pragma unroll
+    for (int a = 0; a < 4; ++a)
+#pragma unroll
+        for (int hi = 0; hi < 2; ++hi) *reinterpret_cast<float4 *>(orow + 32 * hi + 8 * a + 4 * half) = row(a, hi);
+}
+
 // The problem of this block and its (query block, head, batch row).
 #define DMX_ATT_LOCATE(g)                                                                          \
     int bid_ = blockIdx.x;                                                                         \
@@ -134,7 +167,6 @@ __device__ __forceinline__ int att_xcd_block(int bid, const AttProblem &P, bool 
     const float *__restrict__ q = P_.q;                                                            \
     const float *__restrict__ k = P_.k;                                                            \
     const float *__restrict__ v = P_.v;                                                            \
-    float *__restrict__ out = P_.out;                                                              \
     const int64_t ldq = P_.ldq, ldk = P_.ldk, ldv = P_.ldv, ldo = P_.ldo;                          \
     const int64_t q_bs = P_.q_bs, kv_bs = P_.kv_bs, o_bs = P_.o_bs;                                \
     const int n_q = P_.n_q, n_k = P_.n_k;                                                          \
@@ -345,15 +377,8 @@ void attention_kernel(const AttGroup g) {
 
     if (!q_ok) return;
     const float inv = l_run > 0.0f ? 1.0f / l_run : 1.0f;
-    float *orow = out + b * o_bs + (int64_t)qi * ldo + head * ATT_D;
     // Register r of o0/o1 holds dim (0|32) + 8*(r/4) + 4*half + r%4.
-#pragma unroll
-    for (int a = 0; a < 4; ++a) {
-        float4 w0 = make_float4(o0[4 * a] * inv, o0[4 * a + 1] * inv, o0[4 * a + 2] * inv, o0[4 * a + 3] * inv);
-        float4 w1 = make_float4(o1[4 * a] * inv, o1[4 * a + 1] * inv, o1[4 * a + 2] * inv, o1[4 * a + 3] * inv);
-        *reinterpret_cast<float4 *>(orow + 8 * a + 4 * half) = w0;
-        *reinterpret_cast<float4 *>(orow + 32 + 8 * a + 4 * half) = w1;
-    }
+    att_store(P_, b * o_bs + (int64_t)qi * ldo + head * ATT_D, half, o0, o1, inv);
 }
 
 // ---------------------------------------------------------------------------
@@ -540,14 +565,8 @@ __global__ __launch_bounds__(256) void attention_bf16_kernel(const AttGroup g) {
 
     if (!q_ok) return;
     const float inv = l_run > 0.0f ? 1.0f / l_run : 1.0f;
-    float *orow = out + b * o_bs + (int64_t)qi * ldo + head * ATT_D;
-#pragma unroll
-    for (int a = 0; a < 4; ++a) {
-        float4 w0 = make_float4(o0[4 * a] * inv, o0[4 * a + 1] * inv, o0[4 * a + 2] * inv, o0[4 * a + 3] * inv);
-        float4 w1 = make_float4(o1[4 * a] * inv, o1[4 * a + 1] * inv, o1[4 * a + 2] * inv, o1[4 * a + 3] * inv);
-        *reinterpret_cast<float4 *>(orow + 8 * a + 4 * half) = w0;
-        *reinterpret_cast<float4 *>(orow + 32 + 8 * a + 4 * half) = w1;
-    }
+    // Register r of o0/o1 holds dim (0|32) + 8*(r/4) + 4*half + r%4.
+    att_store(P_, b * o_bs + (int64_t)qi * ldo + head * ATT_D, half, o0, o1, inv);
 }
 
 }  // namespace
@@ -564,7 +583,11 @@ void attention_grouped(hipStream_t s, const AttentionArgs *probs, int count, flo
     if (count == 2 && probs[1].n_k > probs[0].n_k) std::swap(order[0], order[1]);
     for (int i = 0; i < count; ++i) {
         const AttentionArgs &a = probs[order[i]];
-        require_ptrs({a.q, a.k, a.v, a.out}, "attention");
+        require_ptrs({a.q, a.k, a.v, a.out_planes.p ? (const void *)a.out_planes.p : (const void *)a.out}, "attention");
+        DMX_REQUIRE(!a.out_planes.p || ((a.out_planes.count == 1 || a.out_planes.count == 3) &&
+                                        (reinterpret_cast<uintptr_t>(a.out_planes.p) & 7) == 0 &&
+                                        a.out_planes.stride % 4 == 0),
+                    "attention: output planes must be 1 or 3, 8-byte aligned");
         DMX_REQUIRE(a.d_head == ATT_D, "attention: only d_head = 64 is implemented");
         DMX_REQUIRE(a.n_q > 0 && a.n_k > 0 && a.batch > 0 && a.heads > 0, "attention: empty problem");
         // K/V tiles are read through buffer resources that end at a (row,
@@ -577,7 +600,7 @@ void attention_grouped(hipStream_t s, const AttentionArgs *probs, int count, flo
                         a.kv_batch_stride % 4 == 0 && a.out_batch_stride % 4 == 0,
                     "attention: row strides must be multiples of 4 floats");
         DMX_REQUIRE(((reinterpret_cast<uintptr_t>(a.q) | reinterpret_cast<uintptr_t>(a.k) |
-                      reinterpret_cast<uintptr_t>(a.v) | reinterpret_cast<uintptr_t>(a.out)) &
+                      reinterpret_cast<uintptr_t>(a.v) | reinterpret_cast<uintptr_t>(a.out_planes.p ? nullptr : a.out)) &
                      15) == 0,
                     "attention: operands must be 16-byte aligned");
         AttProblem &p = g.p[i];
@@ -585,6 +608,9 @@ void attention_grouped(hipStream_t s, const AttentionArgs *probs, int count, flo
         p.k = a.k;
         p.v = a.v;
         p.out = a.out;
+        p.out_planes = a.out_planes.p;
+        p.plane_stride = a.out_planes.stride;
+        p.planes = a.out_planes.count;
         p.ldq = a.ldq;
         p.ldk = a.ldk;
         p.ldv = a.ldv;
@@ -603,7 +629,7 @@ void attention_grouped(hipStream_t s, const AttentionArgs *probs, int count, flo
     }
     DMX_REQUIRE(total < (1ll << 31), "attention: grid too large");
     const dim3 grid((unsigned)total);
-    if (mfma_precision() == MfmaPrecision::BF16)
+    if (bf16_mfma())
         hipLaunchKernelGGL(attention_bf16_kernel, grid, dim3(256), 0, s, g);
     else
         hipLaunchKernelGGL(attention_kernel, grid, dim3(256), 0, s, g);

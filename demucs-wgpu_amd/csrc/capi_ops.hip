@@ -212,8 +212,26 @@ int dmx_op_dconv(void *stream, float *x, int B, int C, int F, int T, int hidden,
 int dmx_op_linear(void *stream, const float *x, int rows, int K, const float *w, const float *bias, int N, int tail,
                   const float *residual, const float *gamma, float *out) {
     return guarded([&] {
-        linear(as_stream(stream), x, K, (int64_t)rows * K, w, bias, 1, rows, K, N, out, N, (int64_t)rows * N,
-               (LinearTail)tail, residual, gamma, nullptr);
+        hipStream_t s = as_stream(stream);
+        const int P = linear_planes();
+        if (P > 0 && rows > 0 && N > 0 && K > 0 && K % 64 == 0) {
+            // The transformer's plane path: x and W split into P bf16 planes
+            // (the runner splits W once at load and has x's producers write
+            // planes), then the plane GEMM.
+            require_ptrs({x, w}, "linear");
+            const int64_t nx = (int64_t)rows * K, nw = (int64_t)N * K;
+            const int64_t sx = (nx + 7) / 8 * 8, sw = (nw + 7) / 8 * 8;
+            Scratch xp((size_t)sx * P * 2), wp((size_t)sw * P * 2);
+            const Planes xpl{static_cast<unsigned short *>(xp.p), sx, P}, wpl{static_cast<unsigned short *>(wp.p), sw, P};
+            split_to_planes(s, x, nx, xpl);
+            split_to_planes(s, w, nw, wpl);
+            linear_planes(s, xpl, K, nx, wpl, bias, 1, rows, K, N, out, Planes{}, N, (int64_t)rows * N,
+                          (LinearTail)tail, residual, gamma, nullptr);
+            DMX_HIP(hipStreamSynchronize(s));
+            return;
+        }
+        linear(s, x, K, (int64_t)rows * K, w, bias, 1, rows, K, N, out, N, (int64_t)rows * N, (LinearTail)tail,
+               residual, gamma, nullptr);
     });
 }
 
@@ -263,8 +281,7 @@ int dmx_op_glu(void *stream, const float *x, int b, int c2, int inner, float *ou
 
 int dmx_op_set_precision(int precision) {
     return guarded([&] {
-        DMX_REQUIRE(precision == DMX_PRECISION_FP32 || precision == DMX_PRECISION_BF16, "unknown precision");
-        mfma_precision() = precision == DMX_PRECISION_BF16 ? MfmaPrecision::BF16 : MfmaPrecision::FP32;
+        mfma_precision() = mfma_of_precision(precision);
     });
 }
 

@@ -40,10 +40,33 @@ inline void require_ptrs(std::initializer_list<const void *> ptrs, const char *w
 // Input precision of the MFMA contractions (GEMMs, attention) that the
 // calling thread launches. The runner sets it per call from its precision;
 // accumulation, softmax, norms and outputs are fp32 either way.
-enum class MfmaPrecision { FP32, BF16 };
+// - FP32: every contraction on the fp32 matrix cores.
+// - FP32X3: the same, except the transformer linears, which run on the bf16
+//   matrix cores over three bf16 planes per operand (gemm_planes.h), an fp32
+//   product to fp32 accuracy.
+// - BF16: contractions take bf16 inputs (the linears one bf16 plane).
+enum class MfmaPrecision { FP32, BF16, FP32X3 };
 inline MfmaPrecision &mfma_precision() {
     static thread_local MfmaPrecision p = MfmaPrecision::FP32;
     return p;
+}
+inline bool bf16_mfma() { return mfma_precision() == MfmaPrecision::BF16; }
+// bf16 planes per operand of the transformer linears (0: fp32 MFMA).
+inline int linear_planes() {
+    switch (mfma_precision()) {
+        case MfmaPrecision::FP32X3: return 3;
+        case MfmaPrecision::BF16: return 1;
+        default: return 0;
+    }
+}
+// A dmx_precision value (dmx.h) as the MFMA precision of what it launches.
+inline MfmaPrecision mfma_of_precision(int precision) {
+    switch (precision) {
+        case 0: return MfmaPrecision::FP32X3;  // DMX_PRECISION_FP32
+        case 1: return MfmaPrecision::BF16;    // DMX_PRECISION_BF16
+        case 2: return MfmaPrecision::FP32;    // DMX_PRECISION_FP32_MFMA
+        default: throw Error(8, "unknown precision " + std::to_string(precision));
+    }
 }
 struct MfmaPrecisionScope {
     MfmaPrecision prev;
@@ -104,6 +127,36 @@ __device__ __forceinline__ int xcd_contiguous(int bid, int total) {
     (void)total;
     return bid;
 #endif
+}
+
+// bf16 planes of fp32 values: x = x_0 + x_1 + ..., x_q the round-to-nearest-
+// even bf16 of what x_0 .. x_{q-1} leave. Each residual is exact in fp32, and
+// each plane carries the next 8 significant bits.
+__device__ __forceinline__ unsigned short bf16_split_step(float &x) {
+    const __bf16 h = (__bf16)x;
+    x -= (float)h;
+    return __builtin_bit_cast(unsigned short, h);
+}
+// Four consecutive values -> P planes, 8 bytes per plane at dst + q * stride.
+template <int P>
+__device__ __forceinline__ void store_planes4(unsigned short *dst, int64_t stride, float4 v) {
+    float r[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+    for (int q = 0; q < P; ++q) {
+        unsigned short h[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) h[e] = bf16_split_step(r[e]);
+        uint2 packed;
+        packed.x = (unsigned)h[0] | ((unsigned)h[1] << 16);
+        packed.y = (unsigned)h[2] | ((unsigned)h[3] << 16);
+        *reinterpret_cast<uint2 *>(dst + q * stride) = packed;
+    }
+}
+// One value -> P planes.
+template <int P>
+__device__ __forceinline__ void store_planes1(unsigned short *dst, int64_t stride, float v) {
+#pragma unroll
+    for (int q = 0; q < P; ++q) dst[q * stride] = bf16_split_step(v);
 }
 
 // Wave64 reductions.

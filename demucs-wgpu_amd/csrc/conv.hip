@@ -3,6 +3,7 @@
 // HBM), GLU-fused rewrites, transposed convolutions as per-phase GEMMs, the
 // fused DConv layer, channel mixers and the transformer linears.
 #include "gemm.h"
+#include "gemm_planes.h"
 #include "ops.h"
 
 namespace dmx {
@@ -591,15 +592,30 @@ struct EpConv2Apply {
     __device__ void finalize(int) {}
 };
 
-// Linear tails on token rows.
+// Linear tails on token rows. With `planes` set (bias or bias + GELU tails
+// only) the results are written as that many bf16 planes, plane_stride
+// apart, for a following linear that reads planes; `out` is then unused.
 struct EpLinear {
     float *out;
     const float *bias, *residual, *gamma;
     double *stats;
     int64_t ldo, batch_stride;
     int tail;
+    unsigned short *planes_out = nullptr;
+    int64_t plane_stride = 0;
+    int planes = 0;
     MomentAcc acc;
     __device__ void init(int) {}
+    __device__ void put(int64_t at, float a) {
+        if (planes_out) {
+            if (planes == 3)
+                store_planes1<3>(planes_out + at, plane_stride, a);
+            else
+                store_planes1<1>(planes_out + at, plane_stride, a);
+        } else {
+            out[at] = a;
+        }
+    }
     __device__ void store(int z, int m, int n, float v) {
         int64_t at = z * batch_stride + (int64_t)m * ldo + n;
         float a = v + bias[n];
@@ -609,7 +625,7 @@ struct EpLinear {
             a = residual[at] + a * gamma[n];
             if (stats) acc.add(a);
         }
-        out[at] = a;
+        put(at, a);
     }
     // A wave's TM x TN fragments of a tile that lies wholly in range:
     // fragment (i, j) register r is row mb + 32 i + 8 (r / 4) + 4 khalf + r % 4,
@@ -642,6 +658,24 @@ struct EpLinear {
                         o[at(i, j, r)] = a;
                     }
                 }
+            }
+        } else if (planes_out) {
+            // Plane outputs, bias (+ GELU) tails.
+            unsigned short *po = planes_out + z * batch_stride;
+#pragma unroll
+            for (int j = 0; j < TN; ++j) {
+                const float bn = bias[nb + 32 * j + col];
+#pragma unroll
+                for (int i = 0; i < TM; ++i)
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) {
+                        float a = v[i][j][r] + bn;
+                        if (tail == TAIL_BIAS_GELU) a = gelu(a);
+                        if (planes == 3)
+                            store_planes1<3>(po + at(i, j, r), plane_stride, a);
+                        else
+                            store_planes1<1>(po + at(i, j, r), plane_stride, a);
+                    }
             }
         } else if (tail == TAIL_BIAS_GELU) {
 #pragma unroll
@@ -742,7 +776,7 @@ void gemm_pick(hipStream_t s, int M, int N, int K, int batches, const AL &al, co
 // scope says so (fp32 accumulation and epilogues either way).
 template <bool GLU, class AL, class BL, class EP>
 void gemm_auto(hipStream_t s, int M, int N, int K, int batches, const AL &al, const BL &bl, const EP &ep) {
-    if (mfma_precision() == MfmaPrecision::BF16)
+    if (bf16_mfma())
         gemm_pick<GLU, true>(s, M, N, K, batches, al, bl, ep);
     else
         gemm_pick<GLU, false>(s, M, N, K, batches, al, bl, ep);
@@ -1106,7 +1140,7 @@ void linear(hipStream_t s, const float *x, int64_t ldx, int64_t x_batch_stride, 
     ep.ldo = ldo;
     ep.batch_stride = out_batch_stride;
     ep.tail = tail;
-    const bool dma_ok = mfma_precision() == MfmaPrecision::FP32 && K % 16 == 0 && aligned16(x) && aligned16(w) &&
+    const bool dma_ok = !bf16_mfma() && K % 16 == 0 && aligned16(x) && aligned16(w) &&
                         ldx % 4 == 0 && x_batch_stride % 4 == 0;
 #if DMX_DMA_STAGES > 0
     if (dma_ok) {
@@ -1118,6 +1152,61 @@ void linear(hipStream_t s, const float *x, int64_t ldx, int64_t x_batch_stride, 
     (void)dma_ok;
 #endif
     gemm_auto<false>(s, M, N, K, batches, kmajor(x, ldx, x_batch_stride), kmajor(w, K, 0), ep);
+}
+
+// Tiles of the plane GEMM: 128 x 128 with two stages of 64-byte k-tiles for
+// three planes (96 KB of LDS, one block per CU) and four-k-group tiles of
+// one plane; 128 x 64 when the 128 x 128 grid would fill fewer than two
+// rounds of the 256 CUs.
+template <class EP>
+void launch_linear_planes(hipStream_t s, int M, int N, int K, int batches, const PlaneRows &al, const PlaneRows &bl,
+                          int P, const EP &ep) {
+    const int64_t tiles = ceil_div((int64_t)M, (int64_t)128) * ceil_div((int64_t)N, (int64_t)128) * batches;
+    const bool narrow = tiles < 512 && N % 64 == 0;
+    if (P == 3) {
+        DMX_REQUIRE(K % 32 == 0, "linear_planes: K must be a multiple of 32");
+        if (narrow)
+            launch_gemm_planes<128, 64, 2, 2, 3, 32>(s, M, N, K, batches, al, bl, ep);
+        else
+            launch_gemm_planes<128, 128, 2, 2, 3, 32>(s, M, N, K, batches, al, bl, ep);
+    } else {
+        DMX_REQUIRE(K % 64 == 0, "linear_planes: K must be a multiple of 64");
+        if (narrow)
+            launch_gemm_planes<128, 64, 2, 3, 1, 64>(s, M, N, K, batches, al, bl, ep);
+        else
+            launch_gemm_planes<128, 128, 2, 2, 1, 64>(s, M, N, K, batches, al, bl, ep);
+    }
+}
+
+void linear_planes(hipStream_t s, Planes x, int64_t ldx, int64_t x_batch_stride, Planes w, const float *bias,
+                   int batches, int M, int K, int N, float *out, Planes out_planes, int64_t ldo,
+                   int64_t out_batch_stride, LinearTail tail, const float *residual, const float *gamma,
+                   double *stats) {
+    require_ptrs({x.p, w.p, bias}, "linear_planes");
+    DMX_REQUIRE(x.count == w.count && (x.count == 1 || x.count == 3), "linear_planes: 1 or 3 planes on both operands");
+    if (out_planes.p) {
+        DMX_REQUIRE(tail != TAIL_RESIDUAL_SCALE && out_planes.count == x.count,
+                    "linear_planes: plane outputs take bias tails and the operands' plane count");
+        DMX_REQUIRE(out_planes.count == 1 || out_planes.stride >= (int64_t)batches * out_batch_stride,
+                    "linear_planes: output planes overlap");
+    } else {
+        require_ptrs({out}, "linear_planes");
+    }
+    if (tail == TAIL_RESIDUAL_SCALE) require_ptrs({residual, gamma}, "linear residual");
+    EpLinear ep;
+    ep.out = out;
+    ep.bias = bias;
+    ep.residual = residual;
+    ep.gamma = gamma;
+    ep.stats = stats;
+    ep.ldo = ldo;
+    ep.batch_stride = out_batch_stride;
+    ep.tail = tail;
+    ep.planes_out = out_planes.p;
+    ep.plane_stride = out_planes.stride;
+    ep.planes = out_planes.count;
+    launch_linear_planes(s, M, N, K, batches, PlaneRows{x.p, ldx, x_batch_stride, x.stride},
+                         PlaneRows{w.p, K, 0, w.stride}, x.count, ep);
 }
 
 void tokens_to_channels(hipStream_t s, const float *tok, int b, int F, int T, int D, const float *w, const float *bias,

@@ -80,6 +80,56 @@ __global__ __launch_bounds__(256) void layer_norm_vec_kernel(const float4 *__res
     }
 }
 
+// layer_norm_vec_kernel with the normalised row written as P bf16 planes
+// (plane q of element i of row r at out + q * stride + r * 4 * DIM4 + i), for
+// the transformer linears that read it.
+template <int V, int P>
+__global__ __launch_bounds__(256) void layer_norm_planes_kernel(const float4 *__restrict__ x, int rows,
+                                                                const float4 *__restrict__ w,
+                                                                const float4 *__restrict__ b,
+                                                                unsigned short *__restrict__ out, int64_t stride) {
+    constexpr int DIM4 = 64 * V;
+    const int row = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+    if (row >= rows) return;
+    const float4 *xr = x + (int64_t)row * DIM4;
+    float4 v[V];
+#pragma unroll
+    for (int j = 0; j < V; ++j) v[j] = xr[lane + 64 * j];
+    float s = 0.0f;
+#pragma unroll
+    for (int j = 0; j < V; ++j) s += (v[j].x + v[j].y) + (v[j].z + v[j].w);
+    const float mean = wave_sum(s) / (float)(4 * DIM4);
+    float q = 0.0f;
+#pragma unroll
+    for (int j = 0; j < V; ++j) {
+        const float a = v[j].x - mean, c = v[j].y - mean, d = v[j].z - mean, e = v[j].w - mean;
+        q += (a * a + c * c) + (d * d + e * e);
+    }
+    const float var = wave_sum(q) / (float)(4 * DIM4);
+    const float inv = 1.0f / sqrtf(var + 1e-5f);
+    unsigned short *orow = out + (int64_t)row * 4 * DIM4;
+#pragma unroll
+    for (int j = 0; j < V; ++j) {
+        const int i = lane + 64 * j;
+        const float4 wv = w[i], bv = b[i];
+        const float4 y = make_float4((v[j].x - mean) * inv * wv.x + bv.x, (v[j].y - mean) * inv * wv.y + bv.y,
+                                     (v[j].z - mean) * inv * wv.z + bv.z, (v[j].w - mean) * inv * wv.w + bv.w);
+        store_planes4<P>(orow + 4 * i, stride, y);
+    }
+}
+
+// x -> P bf16 planes, four values per thread.
+template <int P>
+__global__ __launch_bounds__(256) void split_planes_kernel(const float *__restrict__ x, int64_t n,
+                                                           unsigned short *__restrict__ out, int64_t stride) {
+    const int64_t i = 4 * ((int64_t)blockIdx.x * 256 + threadIdx.x);
+    if (i + 3 < n) {
+        store_planes4<P>(out + i, stride, *reinterpret_cast<const float4 *>(x + i));
+    } else {
+        for (int64_t e = i; e < n; ++e) store_planes1<P>(out + e, stride, x[e]);
+    }
+}
+
 // (b, c, F*T) channel-major -> LayerNorm'd token rows (b, T*F, c), token = t*F + f,
 // plus pos[token] * pos_weight. A block stages TOK_POS positions x all
 // channels in LDS ([c][TOK_POS + 1]: an odd row stride, so a wave reading one
@@ -322,6 +372,43 @@ void layer_norm_rows(hipStream_t s, const float *x, int rows, int dim, const flo
         hipLaunchKernelGGL(layer_norm_kernel, dim3((unsigned)ceil_div(rows, 4)), dim3(256), 0, s, x, rows, dim, w, b,
                            out, add, add ? add_rows : 1);
     }
+    DMX_LAUNCH_CHECK();
+}
+
+void layer_norm_planes(hipStream_t s, const float *x, int rows, int dim, const float *w, const float *b, Planes out) {
+    if (rows <= 0) return;
+    require_ptrs({x, w, b, out.p}, "layer_norm_planes");
+    DMX_REQUIRE(dim == 512, "layer_norm_planes: rows of 512 only");
+    DMX_REQUIRE(((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(w) | reinterpret_cast<uintptr_t>(b)) &
+                 15) == 0 && (reinterpret_cast<uintptr_t>(out.p) & 7) == 0 && out.stride % 4 == 0,
+                "layer_norm_planes: operands must be aligned");
+    DMX_REQUIRE(out.count == 1 || out.count == 3, "layer_norm_planes: 1 or 3 planes");
+    DMX_REQUIRE(out.count == 1 || out.stride >= (int64_t)rows * dim, "layer_norm_planes: planes overlap");
+    auto go = [&](auto kernel) {
+        hipLaunchKernelGGL(kernel, dim3((unsigned)ceil_div(rows, 4)), dim3(256), 0, s,
+                           reinterpret_cast<const float4 *>(x), rows, reinterpret_cast<const float4 *>(w),
+                           reinterpret_cast<const float4 *>(b), out.p, out.stride);
+    };
+    if (out.count == 3)
+        go(layer_norm_planes_kernel<2, 3>);
+    else
+        go(layer_norm_planes_kernel<2, 1>);
+    DMX_LAUNCH_CHECK();
+}
+
+void split_to_planes(hipStream_t s, const float *x, int64_t n, Planes out) {
+    if (n <= 0) return;
+    require_ptrs({x, out.p}, "split_to_planes");
+    DMX_REQUIRE(((reinterpret_cast<uintptr_t>(x) & 15) | (reinterpret_cast<uintptr_t>(out.p) & 7)) == 0 &&
+                    out.stride % 4 == 0,
+                "split_to_planes: operands must be aligned");
+    DMX_REQUIRE(out.count == 1 || out.count == 3, "split_to_planes: 1 or 3 planes");
+    DMX_REQUIRE(out.count == 1 || out.stride >= n, "split_to_planes: planes overlap");
+    const unsigned blocks = (unsigned)ceil_div(ceil_div(n, (int64_t)4), (int64_t)256);
+    if (out.count == 3)
+        hipLaunchKernelGGL(split_planes_kernel<3>, dim3(blocks), dim3(256), 0, s, x, n, out.p, out.stride);
+    else
+        hipLaunchKernelGGL(split_planes_kernel<1>, dim3(blocks), dim3(256), 0, s, x, n, out.p, out.stride);
     DMX_LAUNCH_CHECK();
 }
 

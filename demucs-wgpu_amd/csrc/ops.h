@@ -118,6 +118,28 @@ void linear(hipStream_t s, const float *x, int64_t ldx, int64_t x_batch_stride, 
             int batches, int M, int K, int N, float *out, int64_t ldo, int64_t out_batch_stride, LinearTail tail,
             const float *residual, const float *gamma, double *stats);
 
+// An fp32 operand stored as `count` bf16 planes (x = x_0 + ... + x_{count-1},
+// each plane round-to-nearest-even of what the previous ones leave): plane q
+// of element i is p[q * stride + i]. count = 3 holds every fp32 value
+// exactly; count = 1 is plain bf16.
+struct Planes {
+    unsigned short *p = nullptr;
+    int64_t stride = 0;
+    int count = 0;
+    Planes offset(int64_t elements) const { return Planes{p ? p + elements : nullptr, stride, count}; }
+};
+// x (n floats) -> planes.
+void split_to_planes(hipStream_t s, const float *x, int64_t n, Planes out);
+// linear() over plane operands on the bf16 matrix cores (gemm_planes.h):
+// x rows at z * x_batch_stride + m * ldx of every plane, W (N, K) row-major
+// planes. The result goes to `out` (fp32), or, when out_planes.p is set, to
+// out_planes (same indexing) and `out` is unused. Plane products (i, j) with
+// i + j < count are summed, so count = 3 is an fp32-accurate product.
+void linear_planes(hipStream_t s, Planes x, int64_t ldx, int64_t x_batch_stride, Planes w, const float *bias,
+                   int batches, int M, int K, int N, float *out, Planes out_planes, int64_t ldo,
+                   int64_t out_batch_stride, LinearTail tail, const float *residual, const float *gamma,
+                   double *stats);
+
 // Channel mixer reading transformer tokens: out (b, M, F*T) with
 // out[z][m][f*T + t] = W[m] . tok[z][t*F + f] + bias[m] (F = 1: token = t).
 void tokens_to_channels(hipStream_t s, const float *tok, int b, int F, int T, int D, const float *w, const float *bias,
@@ -142,12 +164,17 @@ struct AttentionArgs {
     int64_t ldo;
     int batch, heads, n_q, n_k, d_head;
     int64_t q_batch_stride, kv_batch_stride, out_batch_stride;
+    // When set, the output goes to these bf16 planes (same indexing as out),
+    // and out is unused.
+    Planes out_planes{};
 };
 void attention_grouped(hipStream_t s, const AttentionArgs *probs, int count, float scale);
 
 // ---------------- norms / elementwise (norm.hip) ----------------
 void layer_norm_rows(hipStream_t s, const float *x, int rows, int dim, const float *w, const float *b, float *out,
                      const float *add, int add_rows);
+// The same (dim = 512, no add) with the output written as bf16 planes.
+void layer_norm_planes(hipStream_t s, const float *x, int rows, int dim, const float *w, const float *b, Planes out);
 // (b, c, positions) channel-major -> token rows (b, T*F, c) reordered token = t*F + f,
 // LayerNorm over c, then + pos[token] (pos may be null).
 void channels_to_tokens_ln(hipStream_t s, const float *x, int b, int c, int F, int T, const float *w,

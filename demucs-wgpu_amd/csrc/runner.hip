@@ -128,6 +128,16 @@ struct DBuf {
 };
 
 DBuf fbuf(hipStream_t s, int64_t n) { return DBuf(s, (size_t)std::max<int64_t>(n, 1) * sizeof(float)); }
+// Plane stride (bf16 elements) of an n-element operand: whole 16-byte rows.
+int64_t plane_stride(int64_t n) { return (n + 7) / 8 * 8; }
+// A buffer for n elements either as fp32 or as P bf16 planes.
+DBuf obuf(hipStream_t s, int64_t n, int P) {
+    return DBuf(s, std::max<size_t>((size_t)std::max<int64_t>(n, 1) * sizeof(float),
+                                    (size_t)plane_stride(n) * P * sizeof(unsigned short)));
+}
+Planes planes_in(const DBuf &b, int64_t n, int P) {
+    return Planes{static_cast<unsigned short *>(b.p), plane_stride(n), P};
+}
 DBuf dbuf(hipStream_t s, int64_t n) { return DBuf(s, (size_t)std::max<int64_t>(n, 1) * sizeof(double)); }
 
 struct Trace {
@@ -155,6 +165,9 @@ struct TLayerW {
     bool cross;
     const float *in_w, *in_b, *out_w, *out_b, *w1, *b1, *w2, *b2;
     const float *n1w, *n1b, *n2w, *n2b, *n3w, *n3b, *now_, *nob, *g1, *g2;
+    // The four linear weights as bf16 planes, when the runner's linears run
+    // on planes (count 0 otherwise).
+    Planes in_wp, out_wp, w1p, w2p;
 };
 
 }  // namespace
@@ -184,6 +197,7 @@ struct dmx_runner {
     dmx_config cfg{};
     int device = 0;
     int precision = 0;
+    int planes = 0;  // bf16 planes per operand of the transformer linears (0: fp32 MFMA)
     hipStream_t stream = nullptr;
     // The waveform branch runs on its own stream beside the spectral one
     // (all default priority); fork/join are event waits on the GPU.
@@ -421,49 +435,91 @@ int64_t projection_floats(const dmx_runner &r, const TLayerW &L, const LayerShap
     return L.cross ? sh.B * sh.Lq * D + sh.B * sh.Lk * 2 * D : sh.B * sh.Lq * 3 * D;
 }
 AttentionArgs attention_inputs(dmx_runner &r, hipStream_t s, const TLayerW &L, const float *xq, const float *xkv,
-                               const LayerShape &sh, float *proj, float *att) {
-    const int D = r.tch, heads = r.cfg.t_heads, B = sh.B;
+                               const LayerShape &sh, float *proj, void *att) {
+    const int D = r.tch, heads = r.cfg.t_heads, B = sh.B, P = r.planes;
     const int64_t Lq = sh.Lq, Lk = sh.Lk;
-    DBuf nq = fbuf(s, B * Lq * D);
-    layer_norm_rows(s, xq, (int)(B * Lq), D, L.n1w, L.n1b, nq.f(), nullptr, 0);
+    AttentionArgs a{};
     if (L.cross) {
-        DBuf nk = fbuf(s, B * Lk * D);
-        layer_norm_rows(s, xkv, (int)(B * Lk), D, L.n2w, L.n2b, nk.f(), nullptr, 0);
         float *q = proj, *kv = proj + B * Lq * D;
-        linear(s, nq.f(), D, Lq * D, L.in_w, L.in_b, B, (int)Lq, D, D, q, D, Lq * D, TAIL_BIAS, nullptr, nullptr,
-               nullptr);
-        linear(s, nk.f(), D, Lk * D, L.in_w + (int64_t)D * D, L.in_b + D, B, (int)Lk, D, 2 * D, kv, 2 * D,
-               Lk * 2 * D, TAIL_BIAS, nullptr, nullptr, nullptr);
-        return AttentionArgs{q,     D,     kv, 2 * D,    kv + D, 2 * D,      att,        D,
-                             B,     heads, (int)Lq, (int)Lk, D / heads, Lq * D, Lk * 2 * D, Lq * D};
+        if (P) {
+            DBuf nq = obuf(s, B * Lq * D, P), nk = obuf(s, B * Lk * D, P);
+            const Planes nqp = planes_in(nq, B * Lq * D, P), nkp = planes_in(nk, B * Lk * D, P);
+            layer_norm_planes(s, xq, (int)(B * Lq), D, L.n1w, L.n1b, nqp);
+            layer_norm_planes(s, xkv, (int)(B * Lk), D, L.n2w, L.n2b, nkp);
+            linear_planes(s, nqp, D, Lq * D, L.in_wp, L.in_b, B, (int)Lq, D, D, q, Planes{}, D, Lq * D, TAIL_BIAS,
+                          nullptr, nullptr, nullptr);
+            linear_planes(s, nkp, D, Lk * D, L.in_wp.offset((int64_t)D * D), L.in_b + D, B, (int)Lk, D, 2 * D, kv,
+                          Planes{}, 2 * D, Lk * 2 * D, TAIL_BIAS, nullptr, nullptr, nullptr);
+        } else {
+            DBuf nq = fbuf(s, B * Lq * D), nk = fbuf(s, B * Lk * D);
+            layer_norm_rows(s, xq, (int)(B * Lq), D, L.n1w, L.n1b, nq.f(), nullptr, 0);
+            layer_norm_rows(s, xkv, (int)(B * Lk), D, L.n2w, L.n2b, nk.f(), nullptr, 0);
+            linear(s, nq.f(), D, Lq * D, L.in_w, L.in_b, B, (int)Lq, D, D, q, D, Lq * D, TAIL_BIAS, nullptr, nullptr,
+                   nullptr);
+            linear(s, nk.f(), D, Lk * D, L.in_w + (int64_t)D * D, L.in_b + D, B, (int)Lk, D, 2 * D, kv, 2 * D,
+                   Lk * 2 * D, TAIL_BIAS, nullptr, nullptr, nullptr);
+        }
+        a = AttentionArgs{q,     D,     kv,      2 * D,   kv + D,    2 * D,  nullptr,    D,
+                          B,     heads, (int)Lq, (int)Lk, D / heads, Lq * D, Lk * 2 * D, Lq * D};
+    } else {
+        if (P) {
+            DBuf nq = obuf(s, B * Lq * D, P);
+            const Planes nqp = planes_in(nq, B * Lq * D, P);
+            layer_norm_planes(s, xq, (int)(B * Lq), D, L.n1w, L.n1b, nqp);
+            linear_planes(s, nqp, D, Lq * D, L.in_wp, L.in_b, B, (int)Lq, D, 3 * D, proj, Planes{}, 3 * D,
+                          Lq * 3 * D, TAIL_BIAS, nullptr, nullptr, nullptr);
+        } else {
+            DBuf nq = fbuf(s, B * Lq * D);
+            layer_norm_rows(s, xq, (int)(B * Lq), D, L.n1w, L.n1b, nq.f(), nullptr, 0);
+            linear(s, nq.f(), D, Lq * D, L.in_w, L.in_b, B, (int)Lq, D, 3 * D, proj, 3 * D, Lq * 3 * D, TAIL_BIAS,
+                   nullptr, nullptr, nullptr);
+        }
+        a = AttentionArgs{proj, 3 * D, proj + D, 3 * D,    proj + 2 * D, 3 * D,          nullptr,        D,
+                          B,    heads, (int)Lq,  (int)Lq,  D / heads,    Lq * 3 * D, Lq * 3 * D, Lq * D};
     }
-    linear(s, nq.f(), D, Lq * D, L.in_w, L.in_b, B, (int)Lq, D, 3 * D, proj, 3 * D, Lq * 3 * D, TAIL_BIAS, nullptr,
-           nullptr, nullptr);
-    return AttentionArgs{proj,  3 * D, proj + D, 3 * D,    proj + 2 * D, 3 * D,          att,            D,
-                         B,     heads, (int)Lq,  (int)Lq,  D / heads,    Lq * 3 * D, Lq * 3 * D, Lq * D};
+    // The attention output feeds the out-projection: planes when it reads planes.
+    if (P)
+        a.out_planes = Planes{static_cast<unsigned short *>(att), plane_stride(B * Lq * D), P};
+    else
+        a.out = static_cast<float *>(att);
+    return a;
 }
 
 // attention_outputs(): out-projection + LayerScale residual, LN2/LN3, FFN,
 // residual, GroupNorm(1) over the plane, on stream s; writes out (B, Lq, D).
+// `att` is what attention_inputs() directed the attention output to.
 void attention_outputs(dmx_runner &r, hipStream_t s, const TLayerW &L, const float *xq, const LayerShape &sh,
-                       const float *att, const std::string &name, float *out) {
-    const int D = r.tch, H = r.hidden, B = sh.B;
+                       const void *att, const std::string &name, float *out) {
+    const int D = r.tch, H = r.hidden, B = sh.B, P = r.planes;
     const int64_t Lq = sh.Lq;
+    const float *nw = L.cross ? L.n3w : L.n2w, *nb = L.cross ? L.n3b : L.n2b;
     DBuf x1 = fbuf(s, B * Lq * D);
-    linear(s, att, D, Lq * D, L.out_w, L.out_b, B, (int)Lq, D, D, x1.f(), D, Lq * D, TAIL_RESIDUAL_SCALE, xq, L.g1,
-           nullptr);
-    DBuf n2 = fbuf(s, B * Lq * D);
-    if (L.cross)
-        layer_norm_rows(s, x1.f(), (int)(B * Lq), D, L.n3w, L.n3b, n2.f(), nullptr, 0);
-    else
-        layer_norm_rows(s, x1.f(), (int)(B * Lq), D, L.n2w, L.n2b, n2.f(), nullptr, 0);
-    DBuf hid = fbuf(s, B * Lq * H);
-    linear(s, n2.f(), D, Lq * D, L.w1, L.b1, B, (int)Lq, D, H, hid.f(), H, Lq * H, TAIL_BIAS_GELU, nullptr, nullptr,
-           nullptr);
     DBuf stats = dbuf(s, 2 * B);
     zero_doubles(s, stats.d(), 2 * B);
-    linear(s, hid.f(), H, Lq * H, L.w2, L.b2, B, (int)Lq, H, D, out, D, Lq * D, TAIL_RESIDUAL_SCALE, x1.f(), L.g2,
-           stats.d());
+    if (P) {
+        const Planes attp{static_cast<unsigned short *>(const_cast<void *>(att)), plane_stride(B * Lq * D), P};
+        linear_planes(s, attp, D, Lq * D, L.out_wp, L.out_b, B, (int)Lq, D, D, x1.f(), Planes{}, D, Lq * D,
+                      TAIL_RESIDUAL_SCALE, xq, L.g1, nullptr);
+        DBuf n2 = obuf(s, B * Lq * D, P);
+        const Planes n2p = planes_in(n2, B * Lq * D, P);
+        layer_norm_planes(s, x1.f(), (int)(B * Lq), D, nw, nb, n2p);
+        DBuf hid = obuf(s, B * Lq * H, P);
+        const Planes hidp = planes_in(hid, B * Lq * H, P);
+        linear_planes(s, n2p, D, Lq * D, L.w1p, L.b1, B, (int)Lq, D, H, nullptr, hidp, H, Lq * H, TAIL_BIAS_GELU,
+                      nullptr, nullptr, nullptr);
+        linear_planes(s, hidp, H, Lq * H, L.w2p, L.b2, B, (int)Lq, H, D, out, Planes{}, D, Lq * D,
+                      TAIL_RESIDUAL_SCALE, x1.f(), L.g2, stats.d());
+    } else {
+        linear(s, static_cast<const float *>(att), D, Lq * D, L.out_w, L.out_b, B, (int)Lq, D, D, x1.f(), D, Lq * D,
+               TAIL_RESIDUAL_SCALE, xq, L.g1, nullptr);
+        DBuf n2 = fbuf(s, B * Lq * D);
+        layer_norm_rows(s, x1.f(), (int)(B * Lq), D, nw, nb, n2.f(), nullptr, 0);
+        DBuf hid = fbuf(s, B * Lq * H);
+        linear(s, n2.f(), D, Lq * D, L.w1, L.b1, B, (int)Lq, D, H, hid.f(), H, Lq * H, TAIL_BIAS_GELU, nullptr,
+               nullptr, nullptr);
+        linear(s, hid.f(), H, Lq * H, L.w2, L.b2, B, (int)Lq, H, D, out, D, Lq * D, TAIL_RESIDUAL_SCALE, x1.f(), L.g2,
+               stats.d());
+    }
     group_norm_tokens_apply(s, out, B, (int)Lq, D, stats.d(), L.now_, L.nob);
     record(r, name, out, {B, Lq, D});
 }
@@ -490,7 +546,7 @@ void transformer_layers(dmx_runner &r, hipStream_t s, DBuf &spec, int64_t Lf, DB
         // Everything both streams touch comes from s's pool, before the fork.
         DBuf ns = fbuf(s, B * Lf * D), nt_ = fbuf(s, (int64_t)B * Lt * D);
         DBuf ps = fbuf(s, projection_floats(r, Ls, shs)), pt = fbuf(s, projection_floats(r, Lt_, sht));
-        DBuf as = fbuf(s, B * Lf * D), at = fbuf(s, (int64_t)B * Lt * D);
+        DBuf as = obuf(s, B * Lf * D, r.planes), at = obuf(s, (int64_t)B * Lt * D, r.planes);
         Branches br(r, s);
         br.fork();
 #if DMX_ATT_SPLIT
@@ -501,25 +557,25 @@ void transformer_layers(dmx_runner &r, hipStream_t s, DBuf &spec, int64_t Lf, DB
         // time-branch chain fills the tail of the spectral attention.
         {
             const AttentionArgs pta =
-                attention_inputs(r, br.t, Lt_, time.f(), cross ? spec.f() : nullptr, sht, pt.f(), at.f());
+                attention_inputs(r, br.t, Lt_, time.f(), cross ? spec.f() : nullptr, sht, pt.f(), at.p);
             attention_grouped(br.t, &pta, 1, scale);
-            attention_outputs(r, br.t, Lt_, time.f(), sht, at.f(), nt, nt_.f());
+            attention_outputs(r, br.t, Lt_, time.f(), sht, at.p, nt, nt_.f());
             const AttentionArgs psa =
-                attention_inputs(r, s, Ls, spec.f(), cross ? time.f() : nullptr, shs, ps.f(), as.f());
+                attention_inputs(r, s, Ls, spec.f(), cross ? time.f() : nullptr, shs, ps.f(), as.p);
             attention_grouped(s, &psa, 1, scale);
-            attention_outputs(r, s, Ls, spec.f(), shs, as.f(), n, ns.f());
+            attention_outputs(r, s, Ls, spec.f(), shs, as.p, n, ns.f());
         }
         br.join();
 #else
         AttentionArgs prob[2];
-        prob[1] = attention_inputs(r, br.t, Lt_, time.f(), cross ? spec.f() : nullptr, sht, pt.f(), at.f());
-        prob[0] = attention_inputs(r, s, Ls, spec.f(), cross ? time.f() : nullptr, shs, ps.f(), as.f());
+        prob[1] = attention_inputs(r, br.t, Lt_, time.f(), cross ? spec.f() : nullptr, sht, pt.f(), at.p);
+        prob[0] = attention_inputs(r, s, Ls, spec.f(), cross ? time.f() : nullptr, shs, ps.f(), as.p);
         br.join();
         attention_grouped(s, prob, 2, scale);
         Branches br2(r, s);
         br2.fork();
-        attention_outputs(r, br2.t, Lt_, time.f(), sht, at.f(), nt, nt_.f());
-        attention_outputs(r, s, Ls, spec.f(), shs, as.f(), n, ns.f());
+        attention_outputs(r, br2.t, Lt_, time.f(), sht, at.p, nt, nt_.f());
+        attention_outputs(r, s, Ls, spec.f(), shs, as.p, n, ns.f());
         br2.join();
 #endif
         spec = std::move(ns);
@@ -552,9 +608,7 @@ void transformer(dmx_runner &r, hipStream_t s, const float *x, const float *xt, 
 // Stack-only entry point: same prologue/layers, outputs rearranged back to
 // (B, D, F, T) / (B, D, Lt) without the channel mixers.
 // The runner's precision as the MFMA input precision of what it launches.
-MfmaPrecision mfma_of(const dmx_runner &r) {
-    return r.precision == DMX_PRECISION_BF16 ? MfmaPrecision::BF16 : MfmaPrecision::FP32;
-}
+MfmaPrecision mfma_of(const dmx_runner &r) { return mfma_of_precision(r.precision); }
 
 void transformer_only(dmx_runner &r, hipStream_t s, const float *x, const float *xt, int B, int F, int T, int Lt,
                       float *x_out, float *xt_out) {
@@ -771,6 +825,33 @@ void forward_device(dmx_runner &r, hipStream_t s, const float *mix, int64_t B, i
 }
 
 // ----- weights -----
+
+// The transformer linears' weights as bf16 planes, split once on the device
+// (one block for all of them).
+void split_linear_weights(dmx_runner &r) {
+    const int P = r.planes, D = r.tch, H = r.hidden;
+    const int64_t sizes[4] = {3LL * D * D, (int64_t)D * D, (int64_t)H * D, (int64_t)D * H};
+    int64_t per_layer = 0;
+    for (int64_t n : sizes) per_layer += plane_stride(n) * P;
+    const size_t n_layers = r.layers.size() + r.layers_t.size();
+    void *mem = nullptr;
+    DMX_HIP(hipMalloc(&mem, std::max<size_t>(n_layers * per_layer * sizeof(unsigned short), 16)));
+    r.owned.push_back(mem);
+    unsigned short *at = static_cast<unsigned short *>(mem);
+    auto take = [&](const float *w, int64_t n) {
+        const Planes p{at, plane_stride(n), P};
+        split_to_planes(r.stream, w, n, p);
+        at += plane_stride(n) * P;
+        return p;
+    };
+    for (auto *v : {&r.layers, &r.layers_t})
+        for (TLayerW &L : *v) {
+            L.in_wp = take(L.in_w, sizes[0]);
+            L.out_wp = take(L.out_w, sizes[1]);
+            L.w1p = take(L.w1, sizes[2]);
+            L.w2p = take(L.w2, sizes[3]);
+        }
+}
 
 void load_weights(dmx_runner &r, const dmx_tensor *weights, size_t n) {
     const dmx_config &c = r.cfg;
@@ -1033,6 +1114,9 @@ void load_weights(dmx_runner &r, const dmx_tensor *weights, size_t n) {
             L.g2 = dev(r, p + ".gamma_2.scale");
             (branch ? r.layers_t : r.layers).push_back(L);
         }
+    // The plane path covers the model's shapes (rows of 512, K a multiple of 64).
+    if (r.tch != 512 || r.hidden % 64 != 0) r.planes = 0;
+    if (r.planes) split_linear_weights(r);
     std::vector<float> tw((size_t)c.nfft / 2 * 2 + c.nfft);
     make_twiddles(c.nfft, tw.data());
     r.twiddles = upload(r, tw);
@@ -1556,7 +1640,8 @@ int dmx_runner_create(const dmx_tensor *weights, size_t n_weights, const dmx_con
     std::unique_ptr<dmx_runner> r(new dmx_runner());
     int rc = guarded([&] {
         if (!weights || !cfg) throw_error(DMX_ERR_ARGUMENT, "null weights or config");
-        if (precision != DMX_PRECISION_FP32 && precision != DMX_PRECISION_BF16)
+        if (precision != DMX_PRECISION_FP32 && precision != DMX_PRECISION_BF16 &&
+            precision != DMX_PRECISION_FP32_MFMA)
             throw_error(DMX_ERR_ARGUMENT, "unknown precision");
         validate(*cfg);
         int count = 0;
@@ -1566,6 +1651,10 @@ int dmx_runner_create(const dmx_tensor *weights, size_t n_weights, const dmx_con
         r->cfg = *cfg;
         r->device = device_ordinal;
         r->precision = precision;
+        {
+            MfmaPrecisionScope prec(mfma_of_precision(precision));
+            r->planes = linear_planes();
+        }
         r->training_length = dmx_config_training_length(cfg);
         r->hop = cfg->nfft / 4;
         DMX_HIP(hipSetDevice(device_ordinal));

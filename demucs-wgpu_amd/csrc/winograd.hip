@@ -231,7 +231,7 @@ static_assert(DMX_WINO_TILE == 0 || DMX_WINO_TILE == 2 || DMX_WINO_TILE == 4, "t
 int winograd_tile(int ic, int C) { return (DMX_WINO_TILE && C >= DMX_WINO_MIN_C && ic % 16 == 0) ? DMX_WINO_TILE : 0; }
 
 bool winograd_applies(int ic, int C, int F, int T) {
-    return winograd_tile(ic, C) && F >= 1 && T >= 1 && mfma_precision() == MfmaPrecision::FP32;
+    return winograd_tile(ic, C) && F >= 1 && T >= 1 && !bf16_mfma();
 }
 
 int64_t winograd_weight_floats(int ic, int C) {

@@ -41,8 +41,16 @@ enum dmx_status {
 };
 
 enum dmx_precision {
-    DMX_PRECISION_FP32 = 0, /* fp32 MFMA everywhere (parity: per-stem SNR >= 60 dB) */
-    DMX_PRECISION_BF16 = 1  /* bf16 MFMA for attention/GEMMs, fp32 softmax/norms/output (>= 40 dB) */
+    /* fp32 results (parity: per-stem SNR >= 60 dB, activations within 1e-3):
+     * convolutions and attention on the fp32 matrix cores; the transformer
+     * linears on the bf16 matrix cores over three bf16 planes per operand
+     * (x = x0 + x1 + x2, all 24 significant bits), an fp32-accurate product. */
+    DMX_PRECISION_FP32 = 0,
+    /* bf16 MFMA inputs for attention/GEMMs, fp32 softmax/norms/output (>= 40 dB) */
+    DMX_PRECISION_BF16 = 1,
+    /* fp32 MFMA for every contraction, the linears included (same parity bar
+     * as DMX_PRECISION_FP32) */
+    DMX_PRECISION_FP32_MFMA = 2
 };
 
 /* One named weight tensor, keyed by its checkpoint name

@@ -21,11 +21,12 @@ extern "C" {
 
 enum { DMX_ACT_NONE = 0, DMX_ACT_GELU = 1 };
 
-/* MFMA input precision (DMX_PRECISION_FP32 / DMX_PRECISION_BF16) of the
- * contractions this thread enqueues through the dmx_op_* entry points below
- * (linear, conv2d, conv2d_glu, conv_transpose, dconv_layer, pointwise,
- * attention); accumulation and every output stay fp32. Per thread, default
- * fp32. The bf16 variant of a runner is chosen at dmx_runner_create instead.
+/* MFMA input precision (a dmx_precision value) of the contractions this
+ * thread enqueues through the dmx_op_* entry points below (linear, conv2d,
+ * conv2d_glu, conv_transpose, dconv_layer, pointwise, attention);
+ * accumulation and every output stay fp32. Per thread, default
+ * DMX_PRECISION_FP32 (dmx_op_linear then splits x and the weight into three
+ * bf16 planes each before the product). The bf16 variant of a runner is chosen at dmx_runner_create instead.
  * No counterpart in the reference, whose device path is fp32 only; it exists
  * so the bf16 kernels can be tested one at a time like the fp32 ones. */
 int dmx_op_set_precision(int precision);

@@ -32,8 +32,13 @@ def per_stem_snr(ref, out):
     return [snr_db(ref[:, s], out[:, s]) for s in range(ref.shape[1])]
 
 
-def test_forward_matches_oracle_per_stem_and_per_activation(dmx, small):
+@pytest.mark.parametrize("precision", ["fp32", "fp32_mfma"])
+def test_forward_matches_oracle_per_stem_and_per_activation(dmx, small, precision):
+    """Both fp32 settings: the default (transformer linears on three bf16
+    planes per operand) and fp32 MFMA for every contraction."""
     cfg, weights, runner, model = small
+    if precision == "fp32_mfma":
+        runner = dmx.Runner(weights, cfg, precision=dmx.PRECISION_FP32_MFMA)
     mix = dmx.signals.gaussian_segments(0, 2, cfg.training_length)
     ref_trace, gpu_trace = {}, {}
     wants = lambda name: name in TRACED

@@ -44,9 +44,18 @@ def call(lib, name, *args):
         raise RuntimeError(f"{name}: {lib.dmx_last_error().decode()}")
 
 
+@pytest.fixture(params=[0, 2], ids=["fp32_planes", "fp32_mfma"])
+def fp32_precision(lib, request):
+    """Both fp32 settings of dmx_op_set_precision: the default (linears on
+    three bf16 planes per operand) and fp32 MFMA everywhere."""
+    assert lib.dmx_op_set_precision(request.param) == 0
+    yield request.param
+    assert lib.dmx_op_set_precision(0) == 0
+
+
 @pytest.mark.parametrize("rows,k,n,tail", [(300, 512, 1536, 0), (37, 19, 70, 0), (64, 512, 2048, 1),
                                            (129, 2048, 512, 2), (2688, 512, 512, 2)])
-def test_linear_matches_oracle(lib, oracle, rows, k, n, tail):
+def test_linear_matches_oracle(lib, oracle, fp32_precision, rows, k, n, tail):
     r = rng(rows + k + n)
     x = r.uniform(-0.4, 0.4, (rows, k)).astype(np.float32)
     w = r.uniform(-0.4, 0.4, (n, k)).astype(np.float32)
@@ -379,6 +388,30 @@ def test_ispec_sum_matches_oracle(lib, oracle, b, L):
     dxs, dxt, dn = dev(xs), dev(xt), dev(norms)
     call(lib, "dmx_op_ispec_sum", stream(), ptr(dxs), ptr(dxt), b, L, ptr(dn), ptr(out))
     assert snr_db(ref, out.cpu().numpy()) > 100
+
+
+@pytest.mark.parametrize("rows,k,n", [(2688, 512, 1536), (1344, 2048, 512), (200, 512, 2048)])
+def test_plane_linear_is_fp32_accurate(lib, rows, k, n):
+    """The three-plane product keeps fp32 accuracy: against a float64
+    reference its worst error is no larger than twice that of the fp32-MFMA
+    kernel on the same operands, and far below a one-plane (bf16) product's.
+    Operands span 2^-20 .. 2^4 in magnitude so that the low planes matter."""
+    r = rng(rows * 3 + k + n)
+    x = (r.standard_normal((rows, k)) * np.exp2(r.uniform(-20, 4, (rows, k)))).astype(np.float32)
+    w = (r.standard_normal((n, k)) * np.exp2(r.uniform(-8, 0, (n, k)))).astype(np.float32)
+    b = np.zeros(n, np.float32)
+    ref = x.astype(np.float64) @ w.T.astype(np.float64)
+    dx, dw, db = dev(x), dev(w), dev(b)
+    errs = {}
+    for prec in (0, 2, 1):
+        assert lib.dmx_op_set_precision(prec) == 0
+        out = torch.empty((rows, n), device="cuda")
+        call(lib, "dmx_op_linear", stream(), ptr(dx), rows, k, ptr(dw), ptr(db), n, 0, None, None, ptr(out))
+        errs[prec] = float(np.abs(out.cpu().numpy().astype(np.float64) - ref).max())
+    assert lib.dmx_op_set_precision(0) == 0
+    scale = float(np.abs(ref).max())
+    assert errs[0] <= 2.0 * errs[2] + 1e-7 * scale, errs
+    assert errs[0] < 1e-2 * errs[1], errs
 
 
 # ---- bf16-MFMA variant: inputs rounded to bf16, fp32 accumulation and output.
