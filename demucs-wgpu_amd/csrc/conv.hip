@@ -1154,27 +1154,37 @@ void linear(hipStream_t s, const float *x, int64_t ldx, int64_t x_batch_stride, 
     gemm_auto<false>(s, M, N, K, batches, kmajor(x, ldx, x_batch_stride), kmajor(w, K, 0), ep);
 }
 
-// Tiles of the plane GEMM: 128 x 128 with two stages of 64-byte k-tiles for
-// three planes (96 KB of LDS, one block per CU) and four-k-group tiles of
-// one plane; 128 x 64 when the 128 x 128 grid would fill fewer than two
-// rounds of the 256 CUs.
+// Tiles of the plane GEMM (MI355X sweeps of the model's shapes). Three
+// planes, 64-byte k-tiles, two stages:
+// - N >= 2048: 256 x 128 on eight waves, N >= 1024: 128 x 256 on eight waves
+//   (144 KB of LDS, one block and two waves per SIMD per CU);
+// - N < 1024: 128 x 128 on eight waves when that grid fills two rounds of
+//   the 256 CUs, else 256 x 128 for long contractions and 128 x 64 on four
+//   waves for short ones.
+// One plane: 128 x 128 (128 x 64 for small grids) on four waves with
+// four-k-group tiles.
 template <class EP>
 void launch_linear_planes(hipStream_t s, int M, int N, int K, int batches, const PlaneRows &al, const PlaneRows &bl,
                           int P, const EP &ep) {
     const int64_t tiles = ceil_div((int64_t)M, (int64_t)128) * ceil_div((int64_t)N, (int64_t)128) * batches;
-    const bool narrow = tiles < 512 && N % 64 == 0;
     if (P == 3) {
         DMX_REQUIRE(K % 32 == 0, "linear_planes: K must be a multiple of 32");
-        if (narrow)
-            launch_gemm_planes<128, 64, 2, 2, 3, 32>(s, M, N, K, batches, al, bl, ep);
+        if (N >= 2048)
+            launch_gemm_planes<256, 128, 4, 2, 3, 32, 8>(s, M, N, K, batches, al, bl, ep);
+        else if (N >= 1024)
+            launch_gemm_planes<128, 256, 2, 2, 3, 32, 8>(s, M, N, K, batches, al, bl, ep);
+        else if (tiles >= 512)
+            launch_gemm_planes<128, 128, 4, 2, 3, 32, 8>(s, M, N, K, batches, al, bl, ep);
+        else if (K >= 2048)
+            launch_gemm_planes<256, 128, 4, 2, 3, 32, 8>(s, M, N, K, batches, al, bl, ep);
         else
-            launch_gemm_planes<128, 128, 2, 2, 3, 32>(s, M, N, K, batches, al, bl, ep);
+            launch_gemm_planes<128, 64, 2, 2, 3, 32, 4>(s, M, N, K, batches, al, bl, ep);
     } else {
         DMX_REQUIRE(K % 64 == 0, "linear_planes: K must be a multiple of 64");
-        if (narrow)
-            launch_gemm_planes<128, 64, 2, 3, 1, 64>(s, M, N, K, batches, al, bl, ep);
+        if (tiles < 512 && N % 64 == 0)
+            launch_gemm_planes<128, 64, 2, 3, 1, 64, 4>(s, M, N, K, batches, al, bl, ep);
         else
-            launch_gemm_planes<128, 128, 2, 2, 1, 64>(s, M, N, K, batches, al, bl, ep);
+            launch_gemm_planes<128, 128, 2, 2, 1, 64, 4>(s, M, N, K, batches, al, bl, ep);
     }
 }
 
@@ -1205,6 +1215,14 @@ void linear_planes(hipStream_t s, Planes x, int64_t ldx, int64_t x_batch_stride,
     ep.planes_out = out_planes.p;
     ep.plane_stride = out_planes.stride;
     ep.planes = out_planes.count;
+    // Batches laid end to end are one taller problem (whole tiles run over
+    // the batch boundaries), unless the epilogue keeps per-batch moments.
+    if (batches > 1 && !stats && x_batch_stride == (int64_t)M * ldx && out_batch_stride == (int64_t)M * ldo &&
+        (int64_t)M * batches < (1LL << 31)) {
+        M *= batches;
+        batches = 1;
+        ep.batch_stride = 0;
+    }
     launch_linear_planes(s, M, N, K, batches, PlaneRows{x.p, ldx, x_batch_stride, x.stride},
                          PlaneRows{w.p, K, 0, w.stride}, x.count, ep);
 }

@@ -105,8 +105,8 @@ __device__ __forceinline__ int planes_swz(int r) {
 #define DMX_PLANES_WPE 2
 #endif
 
-template <int BM, int BN, int WAVES_M, int STAGES, int P, int BK, class EP>
-__global__ __launch_bounds__(GEMM_THREADS) __attribute__((amdgpu_waves_per_eu(DMX_PLANES_WPE))) void gemm_planes_kernel(
+template <int BM, int BN, int WAVES_M, int STAGES, int P, int BK, int NW, class EP>
+__global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(DMX_PLANES_WPE))) void gemm_planes_kernel(
     int M, int N, int K, PlaneRows al, PlaneRows bl, EP ep) {
     static_assert(BK == 16 || BK == 32 || BK == 64, "k-tile of one, two or four MFMA k-groups");
     constexpr int G = BK / 16;              // MFMA k-groups per k-tile
@@ -115,10 +115,11 @@ __global__ __launch_bounds__(GEMM_THREADS) __attribute__((amdgpu_waves_per_eu(DM
     constexpr int AROWS = P * BM;           // staged rows: A planes, then B planes
     constexpr int ROWS = P * (BM + BN);
     constexpr int INSTR = ROWS / RPI;       // DMA instructions per k-tile
-    constexpr int PER_WAVE = INSTR / 4;
+    constexpr int PER_WAVE = INSTR / NW;
     constexpr int STAGE = ROWS * BK;        // bf16 per k-tile
-    static_assert(ROWS % (4 * RPI) == 0, "tile rows must fill whole DMA instructions on every wave");
-    constexpr int WAVES_N = 4 / WAVES_M;
+    static_assert(ROWS % (NW * RPI) == 0, "tile rows must fill whole DMA instructions on every wave");
+    static_assert(NW == 4 || NW == 8, "four or eight waves");
+    constexpr int WAVES_N = NW / WAVES_M;
     constexpr int WTM = BM / WAVES_M, WTN = BN / WAVES_N;
     constexpr int TM = WTM / 32, TN = WTN / 32;
     static_assert(TM >= 1 && TN >= 1, "wave tile must hold at least one 32x32 MFMA tile");
@@ -143,7 +144,7 @@ __global__ __launch_bounds__(GEMM_THREADS) __attribute__((amdgpu_waves_per_eu(DM
     const unsigned short *src[PER_WAVE];
 #pragma unroll
     for (int i = 0; i < PER_WAVE; ++i) {
-        const int r = RPI * (wave + 4 * i) + grow;
+        const int r = RPI * (wave + NW * i) + grow;
         if (r < AROWS)
             src[i] = al.row(z, r / BM, min(m0 + r % BM, M - 1)) + 8 * gchunk;
         else
@@ -151,7 +152,7 @@ __global__ __launch_bounds__(GEMM_THREADS) __attribute__((amdgpu_waves_per_eu(DM
     }
     auto issue = [&](int buf, int k0) {
 #pragma unroll
-        for (int i = 0; i < PER_WAVE; ++i) dma_b128(src[i] + k0, lds + buf * STAGE + (wave + 4 * i) * 512);
+        for (int i = 0; i < PER_WAVE; ++i) dma_b128(src[i] + k0, lds + buf * STAGE + (wave + NW * i) * 512);
     };
 
     floatx16 acc[TM][TN];
@@ -290,7 +291,7 @@ __global__ __launch_bounds__(GEMM_THREADS) __attribute__((amdgpu_waves_per_eu(DM
 
 // Launches gemm_planes_kernel: K a positive multiple of BK, every plane row
 // 16-byte aligned (ld, batch and plane strides multiples of 8 bf16).
-template <int BM, int BN, int WAVES_M, int STAGES, int P, int BK, class EP>
+template <int BM, int BN, int WAVES_M, int STAGES, int P, int BK, int NW = 4, class EP>
 void launch_gemm_planes(hipStream_t stream, int M, int N, int K, int batches, const PlaneRows &al,
                         const PlaneRows &bl, const EP &ep) {
     if (M <= 0 || N <= 0 || batches <= 0) return;
@@ -300,13 +301,13 @@ void launch_gemm_planes(hipStream_t stream, int M, int N, int K, int batches, co
                     (uintptr_t)bl.p % 16 == 0,
                 "gemm_planes: plane rows must be 16-byte aligned");
     constexpr size_t lds = (size_t)STAGES * P * (BM + BN) * BK * sizeof(unsigned short);
-    auto kernel = gemm_planes_kernel<BM, BN, WAVES_M, STAGES, P, BK, EP>;
+    auto kernel = gemm_planes_kernel<BM, BN, WAVES_M, STAGES, P, BK, NW, EP>;
     static const bool lds_ok = hipFuncSetAttribute(reinterpret_cast<const void *>(kernel),
                                                    hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) == hipSuccess;
     DMX_REQUIRE(lds_ok, "gemm_planes: the kernel's LDS limit could not be raised");
     dim3 grid((unsigned)ceil_div(N, BN), (unsigned)ceil_div(M, BM), (unsigned)batches);
     DMX_REQUIRE(grid.y <= 65535 && grid.z <= 65535, "GEMM grid too large");
-    hipLaunchKernelGGL(kernel, grid, dim3(GEMM_THREADS), lds, stream, M, N, K, al, bl, ep);
+    hipLaunchKernelGGL(kernel, grid, dim3(64 * NW), lds, stream, M, N, K, al, bl, ep);
     DMX_LAUNCH_CHECK();
 }
 
