@@ -47,7 +47,7 @@ def load_package():
     return mod
 
 
-def attention_roofline(pkg, torch, batch: int, iters: int):
+def attention_roofline(pkg, torch, batch: int, iters: int, precision: int = 0):
     """Average duration of the fused cross-attention kernel on a cross
     layer's work: both directions of the model's cross shape in one launch
     (Lq = 2688 spectral tokens vs Lk = 1344 waveform tokens, and Lq = 1344 vs
@@ -56,6 +56,7 @@ def attention_roofline(pkg, torch, batch: int, iters: int):
     Returns (ms per launch, algorithmic flops per launch)."""
     from demucs_wgpu_amd import _native
     lib = _native.load()
+    assert lib.dmx_op_set_precision(precision) == 0, lib.dmx_last_error()
     heads, D = 8, 512
     (lq0, lk0), (lq1, lk1) = (2688, 1344), (1344, 2688)
     t = {}
@@ -412,6 +413,39 @@ def profile_workload(pkg, torch, args):
             "ms_per_call": round(ms, 3), "copy_calibration_mib": mib}
 
 
+BF16_MFMA_PEAK_TFLOPS = 2500.0  # MI355X dense bf16
+
+
+def planes_attention(args) -> bool:
+    """Whether the fp32 runs use the three-plane attention kernel (the default
+    precision, unless the DMX_ATT_PLANES=0 tuning switch keeps fp32 MFMA)."""
+    return args.precision == "fp32" and os.environ.get("DMX_ATT_PLANES", "1") != "0"
+
+
+def attention_roofline_record(args, attn_ms, attn_tflops, traffic, traffic_source):
+    """The roofline object of the cross-attention launch. The three-plane
+    kernel's algorithm is six bf16 plane products per fp32 multiply-add on the
+    bf16 matrix cores, so its achieved rate is 6x the fp32-equivalent rate,
+    against the bf16 dense peak; the fp32-MFMA kernel's is the fp32 rate
+    against the fp32 peak."""
+    shape = (f"sum of 4*B*Lq*Lk*512 flops over (Lq, Lk) = (2688, 1344) and (1344, 2688), B={args.batch_chunks}, "
+             f"both directions in one launch (dmx_op_attention_pair); avg {attn_ms:.3f} ms per launch")
+    if planes_attention(args):
+        achieved = 6.0 * attn_tflops
+        return {"bound": "mfma", "achieved": round(achieved, 2), "peak": BF16_MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
+                "frac": round(achieved / BF16_MFMA_PEAK_TFLOPS, 4), "traffic": traffic,
+                "traffic_source": traffic_source,
+                "kernel": "attention_x3_kernel (fused cross-attention, fp32-accurate: Q, K, V and P as three bf16 "
+                          "planes, six plane products per multiply-add on v_mfma_f32_32x32x16_bf16)",
+                "per_launch": "6 x (" + shape + ")",
+                "fp32_equivalent": {"tflops": round(attn_tflops, 2),
+                                    "frac_of_fp32_peak": round(attn_tflops / FP32_MFMA_PEAK_TFLOPS, 4)}}
+    return {"bound": "mfma", "achieved": round(attn_tflops, 2), "peak": FP32_MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
+            "frac": round(attn_tflops / FP32_MFMA_PEAK_TFLOPS, 4), "traffic": traffic,
+            "traffic_source": traffic_source, "kernel": "attention_kernel (fused cross-attention, fp32 MFMA)",
+            "per_launch": shape}
+
+
 def fp32_precision(pkg, args):
     """The runner precision of the fp32 workloads (--precision)."""
     return pkg.PRECISION_FP32_MFMA if args.precision == "fp32_mfma" else pkg.PRECISION_FP32
@@ -448,9 +482,11 @@ def main():
     import torch
     pkg = load_package()
     if args.roofline_only:
-        attn_ms, attn_flops = attention_roofline(pkg, torch, args.batch_chunks, args.attn_iters)
+        attn_ms, attn_flops = attention_roofline(pkg, torch, args.batch_chunks, args.attn_iters,
+                                                 fp32_precision(pkg, args))
         mib = copy_calibration(torch)
-        print(json.dumps({"kernel": "attention_kernel", "avg_ms": round(attn_ms, 4),
+        print(json.dumps({"kernel": "attention_x3_kernel" if planes_attention(args) else "attention_kernel",
+                          "avg_ms": round(attn_ms, 4),
                           "tflops": round(attn_flops / (attn_ms * 1e-3) / 1e12, 2),
                           "flops_per_launch": attn_flops, "copy_calibration_mib": mib}))
         return
@@ -522,16 +558,11 @@ def main():
 
     segment_forward = segment_forward_path(pkg, runner, mix, args.batch_chunks, stems)
 
-    attn_ms, attn_flops = attention_roofline(pkg, torch, args.batch_chunks, args.attn_iters)
+    attn_ms, attn_flops = attention_roofline(pkg, torch, args.batch_chunks, args.attn_iters,
+                                             fp32_precision(pkg, args))
     attn_tflops = attn_flops / (attn_ms * 1e-3) / 1e12
     traffic, traffic_source = measured_traffic()
-    roofline = {"bound": "mfma", "achieved": round(attn_tflops, 2), "peak": FP32_MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
-                "frac": round(attn_tflops / FP32_MFMA_PEAK_TFLOPS, 4), "traffic": traffic,
-                "traffic_source": traffic_source,
-                "kernel": "attention_kernel (fused cross-attention, fp32 MFMA)",
-                "per_launch": f"sum of 4*B*Lq*Lk*512 flops over (Lq, Lk) = (2688, 1344) and (1344, 2688), "
-                              f"B={args.batch_chunks}, both directions in one launch (dmx_op_attention_pair); "
-                              f"avg {attn_ms:.3f} ms per launch"}
+    roofline = attention_roofline_record(args, attn_ms, attn_tflops, traffic, traffic_source)
     line = {
         "metric": "htdemucs x-realtime (audio s / wall s) on 1 MI355X; cross-attn TFLOP/s",
         "value": round(xrt, 2),

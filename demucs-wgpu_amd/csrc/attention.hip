@@ -35,6 +35,7 @@
 //     from finite inputs, and the row maxima then take no canonicalising
 //     v_max per score.
 #include <algorithm>
+#include <cstdlib>
 #include <type_traits>
 #include <utility>
 
@@ -569,7 +570,257 @@ __global__ __launch_bounds__(256) void attention_bf16_kernel(const AttGroup g) {
     att_store(P_, b * o_bs + (int64_t)qi * ldo + head * ATT_D, half, o0, o1, inv);
 }
 
+// ---------------------------------------------------------------------------
+// Three-plane variant: fp32 accuracy on the bf16 matrix cores. Q, K, V and
+// the probabilities P are each held as three bf16 planes (x = x0 + x1 + x2,
+// every fp32 value exactly), and each product sums the six plane products
+// a_i b_j with i + j < 3 on v_mfma_f32_32x32x16_bf16; the dropped ones are
+// below 2^-24 of |a b|. Scores, softmax, running max/sum and O stay fp32 as
+// in the fp32 kernel, with the same transposed layout (S^T = K Q^T, then
+// O^T += V^T P^T with P straight from the score registers).
+// Key tiles are 32 keys, double buffered: the three planes of a K tile and of
+// a V^T tile take 27 KB, so two workgroups (two waves per SIMD) share a CU
+// and one wave's softmax and plane split overlap the other's MFMAs. K is
+// fetched along d as float4 and V along keys (eight keys of one dim per
+// thread), so both land in LDS as 8-byte plane runs without a scalar
+// transpose.
+// ---------------------------------------------------------------------------
+
+constexpr int AX_KT = 32;   // keys per tile
+constexpr int AX_LDK = 72;  // bf16 per K row (144 B: conflict-free b128 reads)
+constexpr int AX_LDV = 36;  // bf16 per V^T row (72 B: conflict-free b64 reads)
+
+// Three bf16 planes of eight fp32 values (round to nearest even at each step).
+__device__ __forceinline__ void split3(floatx8 x, bf16x8 &p0, bf16x8 &p1, bf16x8 &p2) {
+    p0 = __builtin_convertvector(x, bf16x8);
+    x -= __builtin_convertvector(p0, floatx8);
+    p1 = __builtin_convertvector(x, bf16x8);
+    x -= __builtin_convertvector(p1, floatx8);
+    p2 = __builtin_convertvector(x, bf16x8);
+}
+// The same for four values, as bits.
+__device__ __forceinline__ void split3x4(floatx4 x, uint2 (&out)[3]) {
+    typedef __bf16 b4 __attribute__((ext_vector_type(4)));
+#pragma unroll
+    for (int q = 0; q < 3; ++q) {
+        const b4 h = __builtin_convertvector(x, b4);
+        out[q] = __builtin_bit_cast(uint2, h);
+        if (q < 2) x -= __builtin_convertvector(h, floatx4);
+    }
+}
+
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void attention_x3_kernel(const AttGroup g) {
+    DMX_ATT_LOCATE(g)
+    __shared__ __align__(16) __bf16 Ks[2][3][AX_KT][AX_LDK];  // [buffer][plane][key][d]
+    __shared__ __align__(16) __bf16 Vt[2][3][ATT_D][AX_LDV];  // [buffer][plane][d][key]
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int j = lane & 31, half = lane >> 5;
+    const int qi = qblock * (ATT_QW * ATT_WAVES) + wave * ATT_QW + j;
+    const bool q_ok = qi < n_q;
+
+    const float *qb = q + b * q_bs + head * ATT_D;
+    const float *kb = k + b * kv_bs + head * ATT_D;
+    const float *vb = v + b * kv_bs + head * ATT_D;
+
+    // Q planes: dims 16t + 8*half .. +7, pre-scaled into log2 units.
+    bf16x8 qf[3][4];
+    {
+        const float qs = scale * ATT_LOG2E;
+        const float *row = qb + (int64_t)(q_ok ? qi : 0) * ldq + 8 * half;
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            floatx8 x = {};
+            if (q_ok) {
+                const float4 a = *reinterpret_cast<const float4 *>(row + 16 * t);
+                const float4 c = *reinterpret_cast<const float4 *>(row + 16 * t + 4);
+                x = (floatx8){a.x, a.y, a.z, a.w, c.x, c.y, c.z, c.w};
+            }
+            split3(x * qs, qf[0][t], qf[1][t], qf[2][t]);
+        }
+    }
+
+    // Staging. K: slot i of this thread is key (tid + 256 i) / 16, float4
+    // column (tid + 256 i) % 16. V: dim tid % 64 of keys 8 (tid / 64) .. +7.
+    floatx4 kpre[2];
+    float vpre[8];
+    uint32_t kofs[2], vofs[8];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        const int s_ = tid + 256 * i;
+        kofs[i] = (uint32_t)(((s_ >> 4) * ldk + 4 * (s_ & 15)) * sizeof(float));
+    }
+    const int vdim = tid & 63, vkey = 8 * (tid >> 6);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) vofs[i] = (uint32_t)(((vkey + i) * ldv + vdim) * sizeof(float));
+    const uint32_t kbytes = (uint32_t)(((int64_t)(n_k - 1) * ldk + ATT_D) * sizeof(float));
+    const uint32_t vbytes = (uint32_t)(((int64_t)(n_k - 1) * ldv + ATT_D) * sizeof(float));
+    auto fetch = [&](int key0) {
+        const __amdgpu_buffer_rsrc_t rk =
+            att_rsrc(kb + (int64_t)key0 * ldk, kbytes - (uint32_t)(key0 * ldk * sizeof(float)));
+        const __amdgpu_buffer_rsrc_t rv =
+            att_rsrc(vb + (int64_t)key0 * ldv, vbytes - (uint32_t)(key0 * ldv * sizeof(float)));
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+            kpre[i] = __builtin_bit_cast(floatx4, __builtin_amdgcn_raw_buffer_load_b128(rk, kofs[i], 0, 0));
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+            vpre[i] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rv, vofs[i], 0, 0));
+    };
+    auto stage = [&](int buf) {
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const int s_ = tid + 256 * i, key = s_ >> 4, d = 4 * (s_ & 15);
+            uint2 pl[3];
+            split3x4(kpre[i], pl);
+#pragma unroll
+            for (int q = 0; q < 3; ++q) *reinterpret_cast<uint2 *>(&Ks[buf][q][key][d]) = pl[q];
+        }
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            uint2 pl[3];
+            split3x4((floatx4){vpre[4 * h], vpre[4 * h + 1], vpre[4 * h + 2], vpre[4 * h + 3]}, pl);
+#pragma unroll
+            for (int q = 0; q < 3; ++q) *reinterpret_cast<uint2 *>(&Vt[buf][q][vdim][vkey + 4 * h]) = pl[q];
+        }
+    };
+    // V^T operand of plane q for dim row d and keys base + 8(e/4) + 4*half + e%4.
+    auto vfrag = [&](int buf, int q, int d, int base) -> bf16x8 {
+        const bf16x4 lo = *reinterpret_cast<const bf16x4 *>(&Vt[buf][q][d][base + 4 * half]);
+        const bf16x4 hi = *reinterpret_cast<const bf16x4 *>(&Vt[buf][q][d][base + 8 + 4 * half]);
+        return (bf16x8){lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+    };
+
+    const floatx16 zero = {};
+    floatx16 o0 = zero, o1 = zero;
+    float m_run = -INFINITY, l_run = 0.0f;
+    floatx16 negmb = zero;
+    float mb = 0.0f, thr = -INFINITY;
+
+    // One 32-key tile; MASK only for a ragged last tile. Register r of the
+    // scores holds key key0 + 8(r/4) + 4*half + r%4.
+    auto tile = [&](auto mask_tag, int buf, int key0) {
+        constexpr bool MASK = decltype(mask_tag)::value;
+        floatx16 sc = negmb;
+        att_prio(1);
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            bf16x8 kf[3];
+#pragma unroll
+            for (int q = 0; q < 3; ++q) kf[q] = *reinterpret_cast<const bf16x8 *>(&Ks[buf][q][j][16 * t + 8 * half]);
+            // Smallest products first.
+            sc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[2], qf[0][t], sc, 0, 0, 0);
+            sc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[1], qf[1][t], sc, 0, 0, 0);
+            sc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[0], qf[2][t], sc, 0, 0, 0);
+            sc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[1], qf[0][t], sc, 0, 0, 0);
+            sc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[0], qf[1][t], sc, 0, 0, 0);
+            sc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[0], qf[0][t], sc, 0, 0, 0);
+        }
+        if constexpr (MASK) {
+#pragma unroll
+            for (int r = 0; r < 16; ++r)
+                if (key0 + 8 * (r >> 2) + 4 * half + (r & 3) >= n_k) sc[r] = -INFINITY;
+        }
+        att_prio(0);
+        float mloc = sc[0];
+#pragma unroll
+        for (int r = 1; r < 16; ++r) mloc = fmaxf(mloc, sc[r]);
+        mloc = fmaxf(mloc, __shfl_xor(mloc, 32, 64));
+        if (__any(mloc > thr)) {
+            const float m_new = fmaxf(m_run, mloc + mb);
+            const float corr = __builtin_amdgcn_exp2f(m_run - m_new);
+            const float shift = m_new - mb;
+            l_run *= corr;
+            m_run = m_new;
+            mb = m_new;
+            thr = ATT_SLACK;
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                o0[r] *= corr;
+                o1[r] *= corr;
+                sc[r] -= shift;
+                negmb[r] = -m_new;
+            }
+        }
+        float lsum = 0.0f;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            sc[r] = __builtin_amdgcn_exp2f(sc[r]);
+            lsum += sc[r];
+        }
+        lsum += __shfl_xor(lsum, 32, 64);
+        l_run += lsum;
+        // P planes in the B-operand order: registers 8m .. 8m+7.
+        bf16x8 pp[3][2];
+#pragma unroll
+        for (int m = 0; m < 2; ++m)
+            split3((floatx8){sc[8 * m], sc[8 * m + 1], sc[8 * m + 2], sc[8 * m + 3], sc[8 * m + 4], sc[8 * m + 5],
+                             sc[8 * m + 6], sc[8 * m + 7]},
+                   pp[0][m], pp[1][m], pp[2][m]);
+        att_prio(1);
+#pragma unroll
+        for (int m = 0; m < 2; ++m) {
+            bf16x8 va[3], vc[3];
+#pragma unroll
+            for (int q = 0; q < 3; ++q) {
+                va[q] = vfrag(buf, q, j, 16 * m);
+                vc[q] = vfrag(buf, q, 32 + j, 16 * m);
+            }
+            o0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(va[2], pp[0][m], o0, 0, 0, 0);
+            o1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vc[2], pp[0][m], o1, 0, 0, 0);
+            o0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(va[1], pp[1][m], o0, 0, 0, 0);
+            o1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vc[1], pp[1][m], o1, 0, 0, 0);
+            o0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(va[0], pp[2][m], o0, 0, 0, 0);
+            o1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vc[0], pp[2][m], o1, 0, 0, 0);
+            o0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(va[1], pp[0][m], o0, 0, 0, 0);
+            o1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vc[1], pp[0][m], o1, 0, 0, 0);
+            o0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(va[0], pp[1][m], o0, 0, 0, 0);
+            o1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vc[0], pp[1][m], o1, 0, 0, 0);
+            o0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(va[0], pp[0][m], o0, 0, 0, 0);
+            o1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vc[0], pp[0][m], o1, 0, 0, 0);
+        }
+        att_prio(0);
+    };
+
+    const int tiles = (n_k + AX_KT - 1) / AX_KT;
+    const bool ragged = (n_k % AX_KT) != 0;
+    const int full = tiles - (ragged ? 1 : 0);
+    const bool wave_active =
+        qblock * (ATT_QW * ATT_WAVES) + __builtin_amdgcn_readfirstlane(wave) * ATT_QW < n_q;
+    fetch(0);
+    stage(0);
+    __syncthreads();
+    for (int t = 0; t < full; ++t) {
+        const int buf = t & 1;
+        const bool more = t + 1 < tiles;
+        fetch(min(t + 1, tiles - 1) * AX_KT);
+        __builtin_amdgcn_sched_barrier(0);
+        if (wave_active) tile(std::false_type{}, buf, t * AX_KT);
+        if (more) {
+            // The other buffer was last read in tile t-1, which every wave
+            // finished before the previous barrier.
+            stage(buf ^ 1);
+            __syncthreads();
+        }
+    }
+    if (ragged && wave_active) tile(std::true_type{}, full & 1, full * AX_KT);
+
+    if (!q_ok) return;
+    const float inv = l_run > 0.0f ? 1.0f / l_run : 1.0f;
+    att_store(P_, b * o_bs + (int64_t)qi * ldo + head * ATT_D, half, o0, o1, inv);
+}
+
 }  // namespace
+
+// The three-plane kernel serves the fp32 precision unless DMX_ATT_PLANES=0
+// (read once) keeps the fp32-MFMA kernel there.
+bool attention_planes_enabled() {
+    static const bool on = [] {
+        const char *e = std::getenv("DMX_ATT_PLANES");
+        return !e || std::atoi(e) != 0;
+    }();
+    return on;
+}
 
 void attention_grouped(hipStream_t s, const AttentionArgs *probs, int count, float scale) {
     DMX_REQUIRE(count >= 1 && count <= 2, "attention: one or two problems per launch");
@@ -631,6 +882,8 @@ void attention_grouped(hipStream_t s, const AttentionArgs *probs, int count, flo
     const dim3 grid((unsigned)total);
     if (bf16_mfma())
         hipLaunchKernelGGL(attention_bf16_kernel, grid, dim3(256), 0, s, g);
+    else if (mfma_precision() == MfmaPrecision::FP32X3 && attention_planes_enabled())
+        hipLaunchKernelGGL(attention_x3_kernel, grid, dim3(256), 0, s, g);
     else
         hipLaunchKernelGGL(attention_kernel, grid, dim3(256), 0, s, g);
     DMX_LAUNCH_CHECK();

@@ -47,7 +47,7 @@ inline void require_ptrs(std::initializer_list<const void *> ptrs, const char *w
 // - BF16: contractions take bf16 inputs (the linears one bf16 plane).
 enum class MfmaPrecision { FP32, BF16, FP32X3 };
 inline MfmaPrecision &mfma_precision() {
-    static thread_local MfmaPrecision p = MfmaPrecision::FP32;
+    static thread_local MfmaPrecision p = MfmaPrecision::FP32X3;  // DMX_PRECISION_FP32
     return p;
 }
 inline bool bf16_mfma() { return mfma_precision() == MfmaPrecision::BF16; }

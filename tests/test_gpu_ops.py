@@ -243,7 +243,7 @@ def test_dconv_both_layers_matches_oracle(lib, oracle, dmx, B, C, F, T):
 
 
 @pytest.mark.parametrize("batch,heads,nq,nk", [(1, 8, 200, 130), (2, 2, 64, 64), (1, 1, 33, 1), (1, 8, 2688, 1344)])
-def test_attention_matches_oracle(lib, oracle, batch, heads, nq, nk):
+def test_attention_matches_oracle(lib, oracle, fp32_precision, batch, heads, nq, nk):
     r = rng(nq + nk)
     D = heads * 64
     q = r.uniform(-2, 2, (batch, nq, D)).astype(np.float32)
@@ -263,7 +263,7 @@ def test_attention_matches_oracle(lib, oracle, batch, heads, nq, nk):
 
 @pytest.mark.parametrize("batch,heads,nq0,nk0,nq1,nk1", [(2, 2, 200, 70, 70, 200), (1, 8, 2688, 1344, 1344, 2688),
                                                         (3, 1, 33, 5, 129, 129)])
-def test_attention_pair_matches_oracle(lib, oracle, batch, heads, nq0, nk0, nq1, nk1):
+def test_attention_pair_matches_oracle(lib, oracle, fp32_precision, batch, heads, nq0, nk0, nq1, nk1):
     """Two problems in one launch (the blocks of the one with more keys come
     first): each output matches the oracle on its own problem."""
     r = rng(nq0 + 7 * nk1)
@@ -287,7 +287,7 @@ def test_attention_pair_matches_oracle(lib, oracle, batch, heads, nq0, nk0, nq1,
 
 
 @pytest.mark.parametrize("ramp", [1.0, 3.0, -3.0])
-def test_attention_running_max_moves_across_tiles(lib, oracle, ramp):
+def test_attention_running_max_moves_across_tiles(lib, oracle, fp32_precision, ramp):
     """Key norms ramp along the sequence, so each query's row max keeps rising
     (or falls after the first tile) by many times 2^8 in probability: every
     rescale path of the online softmax runs, and the last tile is ragged."""
@@ -411,6 +411,35 @@ def test_plane_linear_is_fp32_accurate(lib, rows, k, n):
     assert lib.dmx_op_set_precision(0) == 0
     scale = float(np.abs(ref).max())
     assert errs[0] <= 2.0 * errs[2] + 1e-7 * scale, errs
+    assert errs[0] < 1e-2 * errs[1], errs
+
+
+@pytest.mark.parametrize("nq,nk", [(2688, 1344), (1344, 2688), (300, 333)])
+def test_plane_attention_is_fp32_accurate(lib, nq, nk):
+    """The three-plane attention keeps fp32 accuracy: against a float64
+    softmax its worst error is at most twice the fp32-MFMA kernel's, and far
+    below the bf16 kernel's."""
+    r = rng(nq + 3 * nk)
+    heads, D = 2, 128
+    q = r.uniform(-2, 2, (1, nq, D)).astype(np.float32)
+    k = r.uniform(-2, 2, (1, nk, D)).astype(np.float32)
+    v = r.uniform(-2, 2, (1, nk, D)).astype(np.float32)
+    ref = np.empty(q.shape, np.float64)
+    for h in range(heads):
+        sl = slice(64 * h, 64 * h + 64)
+        s_ = (q[0, :, sl].astype(np.float64) * 0.125) @ k[0, :, sl].astype(np.float64).T
+        p_ = np.exp(s_ - s_.max(axis=1, keepdims=True))
+        ref[0, :, sl] = (p_ @ v[0, :, sl].astype(np.float64)) / p_.sum(axis=1, keepdims=True)
+    dq, dk, dv = dev(q), dev(k), dev(v)
+    errs = {}
+    for prec in (0, 2, 1):
+        assert lib.dmx_op_set_precision(prec) == 0
+        out = torch.empty(q.shape, device="cuda")
+        call(lib, "dmx_op_attention", stream(), ptr(dq), ptr(dk), ptr(dv), ptr(out), 1, heads, nq, nk,
+             ctypes.c_float(0.125))
+        errs[prec] = float(np.abs(out.cpu().numpy().astype(np.float64) - ref).max())
+    assert lib.dmx_op_set_precision(0) == 0
+    assert errs[0] <= 2.0 * errs[2] + 1e-7, errs
     assert errs[0] < 1e-2 * errs[1], errs
 
 
