@@ -47,7 +47,7 @@ def load_package():
     return mod
 
 
-def attention_roofline(pkg, torch, batch: int, iters: int, precision: int = 0):
+def attention_roofline(pkg, torch, batch: int, iters: int, precision: int = 0, planes: bool = False):
     """Average duration of the fused cross-attention kernel on a cross
     layer's work: both directions of the model's cross shape in one launch
     (Lq = 2688 spectral tokens vs Lk = 1344 waveform tokens, and Lq = 1344 vs
@@ -67,14 +67,29 @@ def attention_roofline(pkg, torch, batch: int, iters: int, precision: int = 0):
         t["o" + name] = torch.empty(batch, lq, D, device="cuda")
     stream = torch.cuda.current_stream()
     P = lambda x: ctypes.c_void_p(x.data_ptr())
-    args = (ctypes.c_void_p(stream.cuda_stream), P(t["q0"]), P(t["k0"]), P(t["v0"]), P(t["o0"]), lq0, lk0,
-            P(t["q1"]), P(t["k1"]), P(t["v1"]), P(t["o1"]), lq1, lk1, batch, heads, ctypes.c_float(0.125))
+    sp = ctypes.c_void_p(stream.cuda_stream)
+    if planes:
+        # The three-plane kernel reads K and V as planes, which the runner's
+        # in-projection writes; here they are made once, outside the timing.
+        for name, lk in (("0", lk0), ("1", lk1)):
+            ldvt = (lk + 31) // 32 * 32
+            t["kp" + name] = torch.empty(3 * batch * lk * D, dtype=torch.int16, device="cuda")
+            t["vt" + name] = torch.empty(3 * batch * D * ldvt, dtype=torch.int16, device="cuda")
+            assert lib.dmx_op_kv_planes(sp, P(t["k" + name]), P(t["v" + name]), batch, heads, lk,
+                                        P(t["kp" + name]), P(t["vt" + name])) == 0, lib.dmx_last_error()
+        fn = lib.dmx_op_attention_pair_planes
+        args = (sp, P(t["q0"]), P(t["kp0"]), P(t["vt0"]), P(t["o0"]), lq0, lk0, P(t["q1"]), P(t["kp1"]),
+                P(t["vt1"]), P(t["o1"]), lq1, lk1, batch, heads, ctypes.c_float(0.125))
+    else:
+        fn = lib.dmx_op_attention_pair
+        args = (sp, P(t["q0"]), P(t["k0"]), P(t["v0"]), P(t["o0"]), lq0, lk0,
+                P(t["q1"]), P(t["k1"]), P(t["v1"]), P(t["o1"]), lq1, lk1, batch, heads, ctypes.c_float(0.125))
     for _ in range(3):
-        assert lib.dmx_op_attention_pair(*args) == 0, lib.dmx_last_error()
+        assert fn(*args) == 0, lib.dmx_last_error()
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     start.record(stream)
     for _ in range(iters):
-        lib.dmx_op_attention_pair(*args)
+        fn(*args)
     end.record(stream)
     end.synchronize()
     ms = start.elapsed_time(end) / iters
@@ -483,7 +498,7 @@ def main():
     pkg = load_package()
     if args.roofline_only:
         attn_ms, attn_flops = attention_roofline(pkg, torch, args.batch_chunks, args.attn_iters,
-                                                 fp32_precision(pkg, args))
+                                                 fp32_precision(pkg, args), planes_attention(args))
         mib = copy_calibration(torch)
         print(json.dumps({"kernel": "attention_x3_kernel" if planes_attention(args) else "attention_kernel",
                           "avg_ms": round(attn_ms, 4),
@@ -559,7 +574,7 @@ def main():
     segment_forward = segment_forward_path(pkg, runner, mix, args.batch_chunks, stems)
 
     attn_ms, attn_flops = attention_roofline(pkg, torch, args.batch_chunks, args.attn_iters,
-                                             fp32_precision(pkg, args))
+                                             fp32_precision(pkg, args), planes_attention(args))
     attn_tflops = attn_flops / (attn_ms * 1e-3) / 1e12
     traffic, traffic_source = measured_traffic()
     roofline = attention_roofline_record(args, attn_ms, attn_tflops, traffic, traffic_source)

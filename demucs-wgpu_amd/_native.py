@@ -103,6 +103,8 @@ SIGNATURES = {
     "dmx_op_pointwise": (_I, [_VP, _VP, _VP, _VP, _I, _I, _I, _I, _VP]),
     "dmx_op_attention": (_I, [_VP, _VP, _VP, _VP, _VP, _I, _I, _I, _I, _F]),
     "dmx_op_attention_pair": (_I, [_VP] + [_VP] * 4 + [_I, _I] + [_VP] * 4 + [_I, _I, _I, _I, _F]),
+    "dmx_op_kv_planes": (_I, [_VP, _VP, _VP, _I, _I, _I, _VP, _VP]),
+    "dmx_op_attention_pair_planes": (_I, [_VP] + [_VP] * 4 + [_I, _I] + [_VP] * 4 + [_I, _I, _I, _I, _F]),
     "dmx_op_layer_norm": (_I, [_VP, _VP, _I, _I, _VP, _VP, _VP]),
     "dmx_op_group_norm": (_I, [_VP, _VP, _I, _I, _I, _I, _VP, _VP, _VP]),
     "dmx_op_glu": (_I, [_VP, _VP, _I, _I, _I, _VP]),

@@ -102,6 +102,8 @@ struct AttProblem {
     unsigned short *out_planes;  // when set: the output as `planes` bf16 planes, plane_stride apart
     int64_t plane_stride;
     int planes;
+    const unsigned short *kp, *vt;  // K / V^T planes (KVPlanes) of the three-plane kernel
+    int64_t kp_ps, kp_bs, kp_ld, vt_ps, ldvt;
     int64_t ldq, ldk, ldv, ldo, q_bs, kv_bs, o_bs;
     int n_q, n_k, heads, qblocks, blocks;
 };
@@ -578,50 +580,54 @@ __global__ __launch_bounds__(256) void attention_bf16_kernel(const AttGroup g) {
 // below 2^-24 of |a b|. Scores, softmax, running max/sum and O stay fp32 as
 // in the fp32 kernel, with the same transposed layout (S^T = K Q^T, then
 // O^T += V^T P^T with P straight from the score registers).
-// Key tiles are 32 keys, double buffered: the three planes of a K tile and of
-// a V^T tile take 27 KB, so two workgroups (two waves per SIMD) share a CU
-// and one wave's softmax and plane split overlap the other's MFMAs. K is
-// fetched along d as float4 and V along keys (eight keys of one dim per
-// thread), so both land in LDS as 8-byte plane runs without a scalar
-// transpose.
+// K and V arrive as planes (KVPlanes: the in-projection's epilogue writes
+// them, once per token, instead of every query block splitting its tiles):
+// K [token][d], V^T [d][token] with each 16-token group in the order 0-3,
+// 8-11, 4-7, 12-15, which is the key order of a lane's B operand, so every
+// operand is one 16-byte LDS read and staging is plain 16-byte copies.
+// Key tiles are 32 keys, double buffered: the three planes of a K tile and a
+// V^T tile take 54 KB, so two workgroups (two waves per SIMD) share a CU.
 // ---------------------------------------------------------------------------
 
 constexpr int AX_KT = 32;   // keys per tile
 constexpr int AX_LDK = 72;  // bf16 per K row (144 B: conflict-free b128 reads)
-constexpr int AX_LDV = 36;  // bf16 per V^T row (72 B: conflict-free b64 reads)
+constexpr int AX_LDV = 40;  // bf16 per V^T row (80 B: conflict-free b128 reads)
 
-// Three bf16 planes of eight fp32 values (round to nearest even at each step).
+// Three bf16 planes of eight fp32 values (round to nearest even at each
+// step). The residual of each step comes from the packed bf16 pair itself
+// (low half << 16, high half & 0xffff0000), one conversion per two values.
 __device__ __forceinline__ void split3(floatx8 x, bf16x8 &p0, bf16x8 &p1, bf16x8 &p2) {
-    p0 = __builtin_convertvector(x, bf16x8);
-    x -= __builtin_convertvector(p0, floatx8);
-    p1 = __builtin_convertvector(x, bf16x8);
-    x -= __builtin_convertvector(p1, floatx8);
-    p2 = __builtin_convertvector(x, bf16x8);
-}
-// The same for four values, as bits.
-__device__ __forceinline__ void split3x4(floatx4 x, uint2 (&out)[3]) {
-    typedef __bf16 b4 __attribute__((ext_vector_type(4)));
+    typedef unsigned uintx4 __attribute__((ext_vector_type(4)));
+    auto step = [](floatx8 &v) {
+        const bf16x8 h = __builtin_convertvector(v, bf16x8);
+        const uintx4 u = __builtin_bit_cast(uintx4, h);
 #pragma unroll
-    for (int q = 0; q < 3; ++q) {
-        const b4 h = __builtin_convertvector(x, b4);
-        out[q] = __builtin_bit_cast(uint2, h);
-        if (q < 2) x -= __builtin_convertvector(h, floatx4);
-    }
+        for (int e = 0; e < 4; ++e) {
+            v[2 * e] -= __builtin_bit_cast(float, u[e] << 16);
+            v[2 * e + 1] -= __builtin_bit_cast(float, u[e] & 0xffff0000u);
+        }
+        return h;
+    };
+    p0 = step(x);
+    p1 = step(x);
+    p2 = __builtin_convertvector(x, bf16x8);
 }
 
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void attention_x3_kernel(const AttGroup g) {
     DMX_ATT_LOCATE(g)
     __shared__ __align__(16) __bf16 Ks[2][3][AX_KT][AX_LDK];  // [buffer][plane][key][d]
-    __shared__ __align__(16) __bf16 Vt[2][3][ATT_D][AX_LDV];  // [buffer][plane][d][key]
+    __shared__ __align__(16) __bf16 Vt[2][3][ATT_D][AX_LDV];  // [buffer][plane][d][key, permuted]
+    (void)k;
+    (void)v;
+    (void)ldk;
+    (void)ldv;
+    (void)kv_bs;
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int j = lane & 31, half = lane >> 5;
     const int qi = qblock * (ATT_QW * ATT_WAVES) + wave * ATT_QW + j;
     const bool q_ok = qi < n_q;
-
     const float *qb = q + b * q_bs + head * ATT_D;
-    const float *kb = k + b * kv_bs + head * ATT_D;
-    const float *vb = v + b * kv_bs + head * ATT_D;
 
     // Q planes: dims 16t + 8*half .. +7, pre-scaled into log2 units.
     bf16x8 qf[3][4];
@@ -640,55 +646,35 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void a
         }
     }
 
-    // Staging. K: slot i of this thread is key (tid + 256 i) / 16, float4
-    // column (tid + 256 i) % 16. V: dim tid % 64 of keys 8 (tid / 64) .. +7.
-    floatx4 kpre[2];
-    float vpre[8];
-    uint32_t kofs[2], vofs[8];
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {
-        const int s_ = tid + 256 * i;
-        kofs[i] = (uint32_t)(((s_ >> 4) * ldk + 4 * (s_ & 15)) * sizeof(float));
-    }
-    const int vdim = tid & 63, vkey = 8 * (tid >> 6);
-#pragma unroll
-    for (int i = 0; i < 8; ++i) vofs[i] = (uint32_t)(((vkey + i) * ldv + vdim) * sizeof(float));
-    const uint32_t kbytes = (uint32_t)(((int64_t)(n_k - 1) * ldk + ATT_D) * sizeof(float));
-    const uint32_t vbytes = (uint32_t)(((int64_t)(n_k - 1) * ldv + ATT_D) * sizeof(float));
+    // Staging: 16-byte chunk slot tid of every plane. K: key tid / 8, dims
+    // 8 (tid % 8) .. +7; V^T: dim tid / 4, stored keys 8 (tid % 4) .. +7.
+    // K rows are read through a buffer resource that ends at this (row,
+    // head)'s last key, so a ragged last tile reads zeros past it; V^T rows
+    // are zero from n_k to ldvt.
+    const unsigned short *kpb = P_.kp + b * P_.kp_bs + head * ATT_D;
+    const unsigned short *vtb = P_.vt + ((int64_t)b * P_.heads + head) * ATT_D * P_.ldvt;
+    const int64_t kld = P_.kp_ld;
+    const uint32_t kofs = (uint32_t)(((tid >> 3) * kld + 8 * (tid & 7)) * sizeof(unsigned short));
+    const uint32_t vofs = (uint32_t)(((tid >> 2) * P_.ldvt + 8 * (tid & 3)) * sizeof(unsigned short));
+    const uint32_t kbytes = (uint32_t)(((int64_t)(n_k - 1) * kld + ATT_D) * sizeof(unsigned short));
+    floatx4 kpre[3], vpre[3];
     auto fetch = [&](int key0) {
-        const __amdgpu_buffer_rsrc_t rk =
-            att_rsrc(kb + (int64_t)key0 * ldk, kbytes - (uint32_t)(key0 * ldk * sizeof(float)));
-        const __amdgpu_buffer_rsrc_t rv =
-            att_rsrc(vb + (int64_t)key0 * ldv, vbytes - (uint32_t)(key0 * ldv * sizeof(float)));
 #pragma unroll
-        for (int i = 0; i < 2; ++i)
-            kpre[i] = __builtin_bit_cast(floatx4, __builtin_amdgcn_raw_buffer_load_b128(rk, kofs[i], 0, 0));
-#pragma unroll
-        for (int i = 0; i < 8; ++i)
-            vpre[i] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rv, vofs[i], 0, 0));
+        for (int pl = 0; pl < 3; ++pl) {
+            const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(
+                const_cast<unsigned short *>(kpb + pl * P_.kp_ps + (int64_t)key0 * kld), (short)0,
+                (int)(kbytes - (uint32_t)(key0 * kld * sizeof(unsigned short))), 0x00020000);
+            kpre[pl] = __builtin_bit_cast(floatx4, __builtin_amdgcn_raw_buffer_load_b128(rk, kofs, 0, 0));
+            vpre[pl] = *reinterpret_cast<const floatx4 *>(
+                reinterpret_cast<const char *>(vtb + pl * P_.vt_ps + key0) + vofs);
+        }
     };
     auto stage = [&](int buf) {
 #pragma unroll
-        for (int i = 0; i < 2; ++i) {
-            const int s_ = tid + 256 * i, key = s_ >> 4, d = 4 * (s_ & 15);
-            uint2 pl[3];
-            split3x4(kpre[i], pl);
-#pragma unroll
-            for (int q = 0; q < 3; ++q) *reinterpret_cast<uint2 *>(&Ks[buf][q][key][d]) = pl[q];
+        for (int pl = 0; pl < 3; ++pl) {
+            *reinterpret_cast<floatx4 *>(&Ks[buf][pl][tid >> 3][8 * (tid & 7)]) = kpre[pl];
+            *reinterpret_cast<floatx4 *>(&Vt[buf][pl][tid >> 2][8 * (tid & 3)]) = vpre[pl];
         }
-#pragma unroll
-        for (int h = 0; h < 2; ++h) {
-            uint2 pl[3];
-            split3x4((floatx4){vpre[4 * h], vpre[4 * h + 1], vpre[4 * h + 2], vpre[4 * h + 3]}, pl);
-#pragma unroll
-            for (int q = 0; q < 3; ++q) *reinterpret_cast<uint2 *>(&Vt[buf][q][vdim][vkey + 4 * h]) = pl[q];
-        }
-    };
-    // V^T operand of plane q for dim row d and keys base + 8(e/4) + 4*half + e%4.
-    auto vfrag = [&](int buf, int q, int d, int base) -> bf16x8 {
-        const bf16x4 lo = *reinterpret_cast<const bf16x4 *>(&Vt[buf][q][d][base + 4 * half]);
-        const bf16x4 hi = *reinterpret_cast<const bf16x4 *>(&Vt[buf][q][d][base + 8 + 4 * half]);
-        return (bf16x8){lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
     };
 
     const floatx16 zero = {};
@@ -707,7 +693,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void a
         for (int t = 0; t < 4; ++t) {
             bf16x8 kf[3];
 #pragma unroll
-            for (int q = 0; q < 3; ++q) kf[q] = *reinterpret_cast<const bf16x8 *>(&Ks[buf][q][j][16 * t + 8 * half]);
+            for (int pl = 0; pl < 3; ++pl)
+                kf[pl] = *reinterpret_cast<const bf16x8 *>(&Ks[buf][pl][j][16 * t + 8 * half]);
             // Smallest products first.
             sc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[2], qf[0][t], sc, 0, 0, 0);
             sc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[1], qf[1][t], sc, 0, 0, 0);
@@ -750,7 +737,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void a
         }
         lsum += __shfl_xor(lsum, 32, 64);
         l_run += lsum;
-        // P planes in the B-operand order: registers 8m .. 8m+7.
+        // P planes in the B-operand order: registers 8m .. 8m+7 are keys
+        // 16m + 4*half + 0..3 and 16m + 8 + 4*half + 0..3, which V^T stores
+        // contiguously at 16m + 8*half.
         bf16x8 pp[3][2];
 #pragma unroll
         for (int m = 0; m < 2; ++m)
@@ -762,9 +751,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void a
         for (int m = 0; m < 2; ++m) {
             bf16x8 va[3], vc[3];
 #pragma unroll
-            for (int q = 0; q < 3; ++q) {
-                va[q] = vfrag(buf, q, j, 16 * m);
-                vc[q] = vfrag(buf, q, 32 + j, 16 * m);
+            for (int pl = 0; pl < 3; ++pl) {
+                va[pl] = *reinterpret_cast<const bf16x8 *>(&Vt[buf][pl][j][16 * m + 8 * half]);
+                vc[pl] = *reinterpret_cast<const bf16x8 *>(&Vt[buf][pl][32 + j][16 * m + 8 * half]);
             }
             o0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(va[2], pp[0][m], o0, 0, 0, 0);
             o1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vc[2], pp[0][m], o1, 0, 0, 0);
@@ -810,6 +799,41 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void a
     att_store(P_, b * o_bs + (int64_t)qi * ldo + head * ATT_D, half, o0, o1, inv);
 }
 
+// fp32 K rows -> K planes, four dims per thread.
+__global__ __launch_bounds__(256) void k_planes_kernel(const float *__restrict__ k, int64_t ldk, int64_t kv_bs,
+                                                       int n_k, int D, unsigned short *__restrict__ out,
+                                                       int64_t stride, int64_t bs, int64_t ld) {
+    const int b = blockIdx.y;
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;  // (token, dim quad)
+    const int quads = D / 4;
+    if (i >= (int64_t)n_k * quads) return;
+    const int64_t t = i / quads;
+    const int d = 4 * (int)(i % quads);
+    const float4 x = *reinterpret_cast<const float4 *>(k + b * kv_bs + t * ldk + d);
+    store_planes4<3>(out + b * bs + t * ld + d, stride, x);
+}
+
+// fp32 V rows -> V^T planes, four stored tokens of one dim per thread (zeros
+// past n_k).
+__global__ __launch_bounds__(256) void vt_planes_kernel(const float *__restrict__ v, int64_t ldv, int64_t kv_bs,
+                                                        int n_k, int D, int64_t ldvt,
+                                                        unsigned short *__restrict__ out, int64_t stride) {
+    const int b = blockIdx.y;
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;  // (column, stored-token quad)
+    const int64_t quads = ldvt / 4;
+    if (i >= (int64_t)D * quads) return;
+    const int col = (int)(i % D);
+    const int64_t pos = 4 * (i / D);
+    float x[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        const int64_t t = vt_token_pos(pos + e);  // the permutation is its own inverse
+        x[e] = t < n_k ? v[b * kv_bs + t * ldv + col] : 0.0f;
+    }
+    // Row (b * heads + h) * 64 + d is b * D + col.
+    store_planes4<3>(out + ((int64_t)b * D + col) * ldvt + pos, stride, make_float4(x[0], x[1], x[2], x[3]));
+}
+
 }  // namespace
 
 // The three-plane kernel serves the fp32 precision unless DMX_ATT_PLANES=0
@@ -832,28 +856,47 @@ void attention_grouped(hipStream_t s, const AttentionArgs *probs, int count, flo
     // the short ones.
     int order[2] = {0, 1};
     if (count == 2 && probs[1].n_k > probs[0].n_k) std::swap(order[0], order[1]);
+    const bool planes = probs[0].kv.k != nullptr;
     for (int i = 0; i < count; ++i) {
         const AttentionArgs &a = probs[order[i]];
-        require_ptrs({a.q, a.k, a.v, a.out_planes.p ? (const void *)a.out_planes.p : (const void *)a.out}, "attention");
+        DMX_REQUIRE((a.kv.k != nullptr) == planes, "attention: both problems of a launch take K/V planes or neither");
+        require_ptrs({a.q, a.out_planes.p ? (const void *)a.out_planes.p : (const void *)a.out}, "attention");
         DMX_REQUIRE(!a.out_planes.p || ((a.out_planes.count == 1 || a.out_planes.count == 3) &&
                                         (reinterpret_cast<uintptr_t>(a.out_planes.p) & 7) == 0 &&
                                         a.out_planes.stride % 4 == 0),
                     "attention: output planes must be 1 or 3, 8-byte aligned");
         DMX_REQUIRE(a.d_head == ATT_D, "attention: only d_head = 64 is implemented");
         DMX_REQUIRE(a.n_q > 0 && a.n_k > 0 && a.batch > 0 && a.heads > 0, "attention: empty problem");
-        // K/V tiles are read through buffer resources that end at a (row,
-        // head)'s last key: rows must not overlap, and the extent must fit
-        // the resource's 31-bit size.
-        DMX_REQUIRE(a.ldk >= ATT_D && a.ldv >= ATT_D, "attention: K/V rows shorter than d_head");
-        DMX_REQUIRE(((int64_t)(a.n_k - 1) * std::max(a.ldk, a.ldv) + ATT_D) * (int64_t)sizeof(float) < (1ll << 31),
-                    "attention: K/V extent of one (row, head) exceeds 2 GiB");
-        DMX_REQUIRE(a.ldq % 4 == 0 && a.ldk % 4 == 0 && a.ldv % 4 == 0 && a.ldo % 4 == 0 && a.q_batch_stride % 4 == 0 &&
-                        a.kv_batch_stride % 4 == 0 && a.out_batch_stride % 4 == 0,
+        DMX_REQUIRE(a.ldq % 4 == 0 && a.ldo % 4 == 0 && a.q_batch_stride % 4 == 0 && a.out_batch_stride % 4 == 0,
                     "attention: row strides must be multiples of 4 floats");
-        DMX_REQUIRE(((reinterpret_cast<uintptr_t>(a.q) | reinterpret_cast<uintptr_t>(a.k) |
-                      reinterpret_cast<uintptr_t>(a.v) | reinterpret_cast<uintptr_t>(a.out_planes.p ? nullptr : a.out)) &
-                     15) == 0,
+        DMX_REQUIRE(((reinterpret_cast<uintptr_t>(a.q) |
+                      reinterpret_cast<uintptr_t>(a.out_planes.p ? nullptr : a.out)) & 15) == 0,
                     "attention: operands must be 16-byte aligned");
+        if (planes) {
+            // K tiles are read through buffer resources that end at a (row,
+            // head)'s last key; V^T rows hold whole 32-key tiles.
+            const KVPlanes &kv = a.kv;
+            require_ptrs({kv.k, kv.vt}, "attention planes");
+            DMX_REQUIRE(kv.ldk >= (int64_t)a.heads * ATT_D && kv.ldvt >= kv_ldvt(a.n_k) && kv.ldvt % 32 == 0,
+                        "attention: K/V planes rows too short");
+            DMX_REQUIRE(((reinterpret_cast<uintptr_t>(kv.k) | reinterpret_cast<uintptr_t>(kv.vt)) & 15) == 0 &&
+                            kv.k_stride % 8 == 0 && kv.k_bs % 8 == 0 && kv.ldk % 8 == 0 && kv.vt_stride % 8 == 0,
+                        "attention: K/V planes must be 16-byte aligned");
+            DMX_REQUIRE(((int64_t)(a.n_k - 1) * kv.ldk + ATT_D) * 2 < (1ll << 31),
+                        "attention: K extent of one (row, head) exceeds 2 GiB");
+        } else {
+            require_ptrs({a.k, a.v}, "attention");
+            // K/V tiles are read through buffer resources that end at a (row,
+            // head)'s last key: rows must not overlap, and the extent must fit
+            // the resource's 31-bit size.
+            DMX_REQUIRE(a.ldk >= ATT_D && a.ldv >= ATT_D, "attention: K/V rows shorter than d_head");
+            DMX_REQUIRE(((int64_t)(a.n_k - 1) * std::max(a.ldk, a.ldv) + ATT_D) * (int64_t)sizeof(float) < (1ll << 31),
+                        "attention: K/V extent of one (row, head) exceeds 2 GiB");
+            DMX_REQUIRE(a.ldk % 4 == 0 && a.ldv % 4 == 0 && a.kv_batch_stride % 4 == 0,
+                        "attention: row strides must be multiples of 4 floats");
+            DMX_REQUIRE(((reinterpret_cast<uintptr_t>(a.k) | reinterpret_cast<uintptr_t>(a.v)) & 15) == 0,
+                        "attention: operands must be 16-byte aligned");
+        }
         AttProblem &p = g.p[i];
         p.q = a.q;
         p.k = a.k;
@@ -862,6 +905,13 @@ void attention_grouped(hipStream_t s, const AttentionArgs *probs, int count, flo
         p.out_planes = a.out_planes.p;
         p.plane_stride = a.out_planes.stride;
         p.planes = a.out_planes.count;
+        p.kp = a.kv.k;
+        p.vt = a.kv.vt;
+        p.kp_ps = a.kv.k_stride;
+        p.kp_bs = a.kv.k_bs;
+        p.kp_ld = a.kv.ldk;
+        p.vt_ps = a.kv.vt_stride;
+        p.ldvt = a.kv.ldvt;
         p.ldq = a.ldq;
         p.ldk = a.ldk;
         p.ldv = a.ldv;
@@ -880,12 +930,32 @@ void attention_grouped(hipStream_t s, const AttentionArgs *probs, int count, flo
     }
     DMX_REQUIRE(total < (1ll << 31), "attention: grid too large");
     const dim3 grid((unsigned)total);
-    if (bf16_mfma())
-        hipLaunchKernelGGL(attention_bf16_kernel, grid, dim3(256), 0, s, g);
-    else if (mfma_precision() == MfmaPrecision::FP32X3 && attention_planes_enabled())
+    if (planes)
         hipLaunchKernelGGL(attention_x3_kernel, grid, dim3(256), 0, s, g);
+    else if (bf16_mfma())
+        hipLaunchKernelGGL(attention_bf16_kernel, grid, dim3(256), 0, s, g);
     else
         hipLaunchKernelGGL(attention_kernel, grid, dim3(256), 0, s, g);
+    DMX_LAUNCH_CHECK();
+}
+
+void kv_to_planes(hipStream_t s, const float *k, int64_t ldk, const float *v, int64_t ldv, int64_t kv_bs, int batch,
+                  int heads, int n_k, const KVPlanes &out) {
+    require_ptrs({k, v, out.k, out.vt}, "kv_to_planes");
+    const int D = heads * ATT_D;
+    DMX_REQUIRE(batch > 0 && n_k > 0 && batch <= 65535, "kv_to_planes: empty or too many batches");
+    DMX_REQUIRE(ldk % 4 == 0 && kv_bs % 4 == 0 && (reinterpret_cast<uintptr_t>(k) & 15) == 0,
+                "kv_to_planes: K rows must be float4 aligned");
+    DMX_REQUIRE(out.ldk >= D && out.ldvt >= kv_ldvt(n_k) && out.ldvt % 32 == 0 && out.k_stride % 4 == 0 &&
+                    out.k_bs % 4 == 0 && out.ldk % 4 == 0 && out.vt_stride % 4 == 0 &&
+                    ((reinterpret_cast<uintptr_t>(out.k) | reinterpret_cast<uintptr_t>(out.vt)) & 7) == 0,
+                "kv_to_planes: output layout");
+    const int64_t kq = (int64_t)n_k * (D / 4), vq = (int64_t)D * (out.ldvt / 4);
+    hipLaunchKernelGGL(k_planes_kernel, dim3((unsigned)ceil_div(kq, (int64_t)256), (unsigned)batch), dim3(256), 0, s,
+                       k, ldk, kv_bs, n_k, D, out.k, out.k_stride, out.k_bs, out.ldk);
+    DMX_LAUNCH_CHECK();
+    hipLaunchKernelGGL(vt_planes_kernel, dim3((unsigned)ceil_div(vq, (int64_t)256), (unsigned)batch), dim3(256), 0, s,
+                       v, ldv, kv_bs, n_k, D, out.ldvt, out.vt, out.vt_stride);
     DMX_LAUNCH_CHECK();
 }
 

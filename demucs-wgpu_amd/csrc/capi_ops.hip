@@ -96,6 +96,42 @@ unsigned char *scratch_on_current_device() {
 
 }  // namespace
 
+namespace {
+
+// The K/V planes layout of dmx_op_kv_planes for (batch, heads, n_k):
+// K planes [3][batch][n_k][D], V^T planes [3][batch * D][ldvt].
+KVPlanes op_kv_layout(unsigned short *kp, unsigned short *vtp, int batch, int heads, int n_k) {
+    const int64_t D = (int64_t)heads * 64, ldvt = kv_ldvt(n_k);
+    KVPlanes kv;
+    kv.k = kp;
+    kv.vt = vtp;
+    kv.ldk = D;
+    kv.k_bs = (int64_t)n_k * D;
+    kv.k_stride = (int64_t)batch * n_k * D;
+    kv.ldvt = ldvt;
+    kv.vt_stride = (int64_t)batch * D * ldvt;
+    return kv;
+}
+
+// Scratch planes of one problem's K and V, filled from fp32 K and V.
+struct OpKV {
+    std::unique_ptr<Scratch> k, vt;
+    KVPlanes kv;
+    OpKV(hipStream_t s, const float *kf, const float *vf, int batch, int heads, int n_k) {
+        require_ptrs({kf, vf}, "attention");
+        const int64_t D = (int64_t)heads * 64;
+        DMX_REQUIRE(batch > 0 && heads > 0 && n_k > 0, "attention: empty problem");
+        k.reset(new Scratch((size_t)3 * batch * n_k * D * 2));
+        vt.reset(new Scratch((size_t)3 * batch * D * kv_ldvt(n_k) * 2));
+        kv = op_kv_layout(static_cast<unsigned short *>(k->p), static_cast<unsigned short *>(vt->p), batch, heads, n_k);
+        kv_to_planes(s, kf, D, vf, D, (int64_t)n_k * D, batch, heads, n_k, kv);
+    }
+};
+
+bool op_attention_planes() { return mfma_precision() == MfmaPrecision::FP32X3 && attention_planes_enabled(); }
+
+}  // namespace
+
 extern "C" {
 
 int dmx_op_conv2d(void *stream, const float *x, const float *skip, int b, int ic, int h, int w, const float *weight,
@@ -243,9 +279,17 @@ int dmx_op_pointwise(void *stream, const float *w, const float *bias, const floa
 int dmx_op_attention(void *stream, const float *q, const float *k, const float *v, float *out, int batch, int heads,
                      int n_q, int n_k, float scale) {
     return guarded([&] {
+        hipStream_t s = as_stream(stream);
         int64_t D = (int64_t)heads * 64;
-        attention(as_stream(stream), q, D, k, D, v, D, out, D, batch, heads, n_q, n_k, 64, scale, n_q * D, n_k * D,
-                  n_q * D);
+        AttentionArgs a{q, D, k, D, v, D, out, D, batch, heads, n_q, n_k, 64, n_q * D, n_k * D, n_q * D};
+        if (op_attention_planes()) {
+            OpKV kv(s, k, v, batch, heads, n_k);
+            a.kv = kv.kv;
+            attention_grouped(s, &a, 1, scale);
+            DMX_HIP(hipStreamSynchronize(s));
+            return;
+        }
+        attention_grouped(s, &a, 1, scale);
     });
 }
 
@@ -253,10 +297,45 @@ int dmx_op_attention_pair(void *stream, const float *q0, const float *k0, const 
                           int n_k0, const float *q1, const float *k1, const float *v1, float *out1, int n_q1,
                           int n_k1, int batch, int heads, float scale) {
     return guarded([&] {
+        hipStream_t s = as_stream(stream);
         const int64_t D = (int64_t)heads * 64;
-        const AttentionArgs p[2] = {
+        AttentionArgs p[2] = {
             {q0, D, k0, D, v0, D, out0, D, batch, heads, n_q0, n_k0, 64, n_q0 * D, n_k0 * D, n_q0 * D},
             {q1, D, k1, D, v1, D, out1, D, batch, heads, n_q1, n_k1, 64, n_q1 * D, n_k1 * D, n_q1 * D}};
+        if (op_attention_planes()) {
+            OpKV kv0(s, k0, v0, batch, heads, n_k0), kv1(s, k1, v1, batch, heads, n_k1);
+            p[0].kv = kv0.kv;
+            p[1].kv = kv1.kv;
+            attention_grouped(s, p, 2, scale);
+            DMX_HIP(hipStreamSynchronize(s));
+            return;
+        }
+        attention_grouped(s, p, 2, scale);
+    });
+}
+
+int dmx_op_kv_planes(void *stream, const float *k, const float *v, int batch, int heads, int n_k,
+                     unsigned short *k_planes, unsigned short *vt_planes) {
+    return guarded([&] {
+        require_ptrs({k, v, k_planes, vt_planes}, "kv_planes");
+        DMX_REQUIRE(batch > 0 && heads > 0 && n_k > 0, "kv_planes: empty problem");
+        const int64_t D = (int64_t)heads * 64;
+        kv_to_planes(as_stream(stream), k, D, v, D, (int64_t)n_k * D, batch, heads, n_k,
+                     op_kv_layout(k_planes, vt_planes, batch, heads, n_k));
+    });
+}
+
+int dmx_op_attention_pair_planes(void *stream, const float *q0, unsigned short *kp0, unsigned short *vtp0,
+                                 float *out0, int n_q0, int n_k0, const float *q1, unsigned short *kp1,
+                                 unsigned short *vtp1, float *out1, int n_q1, int n_k1, int batch, int heads,
+                                 float scale) {
+    return guarded([&] {
+        const int64_t D = (int64_t)heads * 64;
+        AttentionArgs p[2] = {
+            {q0, D, nullptr, D, nullptr, D, out0, D, batch, heads, n_q0, n_k0, 64, n_q0 * D, n_k0 * D, n_q0 * D},
+            {q1, D, nullptr, D, nullptr, D, out1, D, batch, heads, n_q1, n_k1, 64, n_q1 * D, n_k1 * D, n_q1 * D}};
+        p[0].kv = op_kv_layout(kp0, vtp0, batch, heads, n_k0);
+        p[1].kv = op_kv_layout(kp1, vtp1, batch, heads, n_k1);
         attention_grouped(as_stream(stream), p, 2, scale);
     });
 }

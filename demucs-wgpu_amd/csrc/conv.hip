@@ -1154,6 +1154,68 @@ void linear(hipStream_t s, const float *x, int64_t ldx, int64_t x_batch_stride, 
     gemm_auto<false>(s, M, N, K, batches, kmajor(x, ldx, x_batch_stride), kmajor(w, K, 0), ep);
 }
 
+// The in-projection's tail for the three-plane attention: column n of row m
+// (token m of batch z) plus bias goes to q (fp32 rows of D) for n < q_cols,
+// to the K planes for the next D columns and to the V^T planes for the last
+// D (KVPlanes layout). Fragment columns lie in one of the three ranges, D
+// being a multiple of 32; four consecutive fragment rows are four tokens
+// that stay adjacent in the V^T token order.
+struct EpQKV {
+    float *q;
+    int64_t q_bs;
+    const float *bias;
+    KVPlanes kv;
+    int q_cols, D;
+    __device__ void init(int) {}
+    __device__ void finalize(int) {}
+    __device__ void store(int z, int m, int n, float v) {
+        const float a = v + bias[n];
+        if (n < q_cols) {
+            q[z * q_bs + (int64_t)m * D + n] = a;
+        } else if (n < q_cols + D) {
+            store_planes1<3>(kv.k + z * kv.k_bs + (int64_t)m * kv.ldk + (n - q_cols), kv.k_stride, a);
+        } else {
+            const int c = n - q_cols - D;
+            store_planes1<3>(kv.vt + ((int64_t)z * D + c) * kv.ldvt + vt_token_pos(m), kv.vt_stride, a);
+        }
+    }
+    template <int TM, int TN>
+    __device__ void store_frags(int z, int mb, int nb, int col, int khalf, const floatx16 (&v)[TM][TN]) {
+#pragma unroll
+        for (int j = 0; j < TN; ++j) {
+            const int n = nb + 32 * j + col;
+            const float bn = bias[n];
+            if (n < q_cols) {
+                float *o = q + z * q_bs + n;
+#pragma unroll
+                for (int i = 0; i < TM; ++i)
+#pragma unroll
+                    for (int r = 0; r < 16; ++r)
+                        o[(int64_t)(mb + 32 * i + 8 * (r / 4) + 4 * khalf + r % 4) * D] = v[i][j][r] + bn;
+            } else if (n < q_cols + D) {
+                unsigned short *o = kv.k + z * kv.k_bs + (n - q_cols);
+#pragma unroll
+                for (int i = 0; i < TM; ++i)
+#pragma unroll
+                    for (int r = 0; r < 16; ++r)
+                        store_planes1<3>(o + (int64_t)(mb + 32 * i + 8 * (r / 4) + 4 * khalf + r % 4) * kv.ldk,
+                                         kv.k_stride, v[i][j][r] + bn);
+            } else {
+                unsigned short *o = kv.vt + ((int64_t)z * D + (n - q_cols - D)) * kv.ldvt;
+#pragma unroll
+                for (int i = 0; i < TM; ++i)
+#pragma unroll
+                    for (int a4 = 0; a4 < 4; ++a4) {
+                        const int t0 = mb + 32 * i + 8 * a4 + 4 * khalf;
+                        store_planes4<3>(o + vt_token_pos(t0), kv.vt_stride,
+                                         make_float4(v[i][j][4 * a4] + bn, v[i][j][4 * a4 + 1] + bn,
+                                                     v[i][j][4 * a4 + 2] + bn, v[i][j][4 * a4 + 3] + bn));
+                    }
+            }
+        }
+    }
+};
+
 // Tiles of the plane GEMM (MI355X sweeps of the model's shapes). Three
 // planes, 64-byte k-tiles, two stages:
 // - N >= 2048: 256 x 128 on eight waves, N >= 1024: 128 x 256 on eight waves
@@ -1225,6 +1287,29 @@ void linear_planes(hipStream_t s, Planes x, int64_t ldx, int64_t x_batch_stride,
     }
     launch_linear_planes(s, M, N, K, batches, PlaneRows{x.p, ldx, x_batch_stride, x.stride},
                          PlaneRows{w.p, K, 0, w.stride}, x.count, ep);
+}
+
+void linear_qkv_planes(hipStream_t s, Planes x, int64_t ldx, int64_t x_batch_stride, Planes w, const float *bias,
+                       int batches, int M, int K, int N, int q_cols, float *q, const KVPlanes &kv) {
+    require_ptrs({x.p, w.p, bias, kv.k, kv.vt}, "linear_qkv_planes");
+    DMX_REQUIRE(x.count == 3 && w.count == 3, "linear_qkv_planes: three planes");
+    DMX_REQUIRE(q_cols == 0 || q, "linear_qkv_planes: q output missing");
+    const int D = (N - q_cols) / 2;
+    DMX_REQUIRE(D > 0 && D % 64 == 0 && (q_cols == 0 || q_cols == D) && q_cols + 2 * D == N,
+                "linear_qkv_planes: columns must be [q |] k | v with D a multiple of 64");
+    DMX_REQUIRE(kv.ldk >= D && kv.ldvt >= kv_ldvt(M) && kv.ldvt % 32 == 0 && kv.k_stride % 4 == 0 &&
+                    kv.k_bs % 4 == 0 && kv.ldk % 4 == 0 && kv.vt_stride % 4 == 0 &&
+                    ((reinterpret_cast<uintptr_t>(kv.k) | reinterpret_cast<uintptr_t>(kv.vt)) & 7) == 0,
+                "linear_qkv_planes: K/V planes layout");
+    EpQKV ep;
+    ep.q = q;
+    ep.q_bs = (int64_t)M * D;
+    ep.bias = bias;
+    ep.kv = kv;
+    ep.q_cols = q_cols;
+    ep.D = D;
+    launch_linear_planes(s, M, N, K, batches, PlaneRows{x.p, ldx, x_batch_stride, x.stride},
+                         PlaneRows{w.p, K, 0, w.stride}, 3, ep);
 }
 
 void tokens_to_channels(hipStream_t s, const float *tok, int b, int F, int T, int D, const float *w, const float *bias,

@@ -128,6 +128,18 @@ struct Planes {
     int count = 0;
     Planes offset(int64_t elements) const { return Planes{p ? p + elements : nullptr, stride, count}; }
 };
+// K and V of one attention problem as the three-plane kernel reads them:
+// K planes [plane][b][token][ldk] (head h at column 64 h); V^T planes
+// [plane][(b * heads + h) * 64 + d][ldvt], tokens of every 16-token group
+// stored in the order 0-3, 8-11, 4-7, 12-15 (vt_token_pos: bits 2 and 3
+// swapped), zeros from n_k up to ldvt, a multiple of 32.
+struct KVPlanes {
+    unsigned short *k = nullptr, *vt = nullptr;
+    int64_t k_stride = 0, k_bs = 0, ldk = 0;  // plane, batch and row strides (bf16 elements)
+    int64_t vt_stride = 0, ldvt = 0;          // plane and row strides
+};
+__host__ __device__ inline int64_t vt_token_pos(int64_t t) { return (t & ~int64_t(12)) | ((t & 4) << 1) | ((t & 8) >> 1); }
+inline int64_t kv_ldvt(int64_t n_k) { return (n_k + 31) / 32 * 32; }
 // x (n floats) -> planes.
 void split_to_planes(hipStream_t s, const float *x, int64_t n, Planes out);
 // linear() over plane operands on the bf16 matrix cores (gemm_planes.h):
@@ -139,6 +151,14 @@ void linear_planes(hipStream_t s, Planes x, int64_t ldx, int64_t x_batch_stride,
                    int batches, int M, int K, int N, float *out, Planes out_planes, int64_t ldo,
                    int64_t out_batch_stride, LinearTail tail, const float *residual, const float *gamma,
                    double *stats);
+
+// The attention in-projection on planes for the three-plane attention: the
+// N = q_cols + 2 D output columns of token m of batch z (plus bias) go to q
+// (fp32, z * M * D + m * D) for the first q_cols (0 or D), then to the K and
+// V^T planes of `kv` (KVPlanes layout, V^T rows of kv.ldvt >= M rounded up
+// to 32, whose padding the caller zeroes when M is not a multiple of 32).
+void linear_qkv_planes(hipStream_t s, Planes x, int64_t ldx, int64_t x_batch_stride, Planes w, const float *bias,
+                       int batches, int M, int K, int N, int q_cols, float *q, const KVPlanes &kv);
 
 // Channel mixer reading transformer tokens: out (b, M, F*T) with
 // out[z][m][f*T + t] = W[m] . tok[z][t*F + f] + bias[m] (F = 1: token = t).
@@ -153,6 +173,13 @@ void attention(hipStream_t s, const float *q, int64_t ldq, const float *k, int64
                int64_t q_batch_stride, int64_t kv_batch_stride, int64_t out_batch_stride);
 // Up to two independent problems (same scale) in one launch, e.g. the two
 // branches of a transformer layer; each as the arguments of attention().
+// fp32 K / V rows (b * kv_bs + token * ld + 64 h + d) -> KVPlanes.
+void kv_to_planes(hipStream_t s, const float *k, int64_t ldk, const float *v, int64_t ldv, int64_t kv_bs, int batch,
+                  int heads, int n_k, const KVPlanes &out);
+// Whether the fp32 precision's attention runs on the three-plane kernel
+// (DMX_ATT_PLANES=0 keeps the fp32-MFMA kernel).
+bool attention_planes_enabled();
+
 struct AttentionArgs {
     const float *q;
     int64_t ldq;
@@ -167,6 +194,9 @@ struct AttentionArgs {
     // When set, the output goes to these bf16 planes (same indexing as out),
     // and out is unused.
     Planes out_planes{};
+    // When set, K and V come from these planes (the three-plane kernel; k, v,
+    // ldk, ldv and kv_batch_stride are unused).
+    KVPlanes kv{};
 };
 void attention_grouped(hipStream_t s, const AttentionArgs *probs, int count, float scale);
 

@@ -430,8 +430,31 @@ struct LayerShape {
     int64_t Lq, Lk;  // Lk = Lq for self-attention
     int B;
 };
+// Whether the layer's attention runs on the three-plane kernel, with the
+// in-projection writing K and V as planes.
+bool kv_planes(const dmx_runner &r) { return r.planes == 3 && attention_planes_enabled(); }
+// The in-projection output for the three-plane attention inside `proj`: q
+// (B, Lq, D) fp32, then the K planes [3][B][Lk][D], then the V^T planes
+// [3][B * D][ldvt] (KVPlanes).
+KVPlanes kv_layout(float *proj, int D, const LayerShape &sh) {
+    const int64_t ldvt = kv_ldvt(sh.Lk);
+    KVPlanes kv;
+    kv.k = reinterpret_cast<unsigned short *>(proj + (int64_t)sh.B * sh.Lq * D);
+    kv.ldk = D;
+    kv.k_bs = sh.Lk * D;
+    kv.k_stride = (int64_t)sh.B * sh.Lk * D;
+    kv.vt = kv.k + 3 * kv.k_stride;
+    kv.ldvt = ldvt;
+    kv.vt_stride = (int64_t)sh.B * D * ldvt;
+    return kv;
+}
 int64_t projection_floats(const dmx_runner &r, const TLayerW &L, const LayerShape &sh) {
     const int D = r.tch;
+    if (kv_planes(r)) {
+        // q, then 3 K planes and 3 V^T planes of bf16 (half a float each).
+        const int64_t halves = 3 * (int64_t)sh.B * sh.Lk * D + 3 * (int64_t)sh.B * D * kv_ldvt(sh.Lk);
+        return (int64_t)sh.B * sh.Lq * D + (halves + 1) / 2;
+    }
     return L.cross ? sh.B * sh.Lq * D + sh.B * sh.Lk * 2 * D : sh.B * sh.Lq * 3 * D;
 }
 AttentionArgs attention_inputs(dmx_runner &r, hipStream_t s, const TLayerW &L, const float *xq, const float *xkv,
@@ -439,7 +462,29 @@ AttentionArgs attention_inputs(dmx_runner &r, hipStream_t s, const TLayerW &L, c
     const int D = r.tch, heads = r.cfg.t_heads, B = sh.B, P = r.planes;
     const int64_t Lq = sh.Lq, Lk = sh.Lk;
     AttentionArgs a{};
-    if (L.cross) {
+    if (kv_planes(r)) {
+        // LN1 (LN2 of the key/value plane) as planes, then the in-projection
+        // straight into q and the K / V^T planes of the three-plane kernel.
+        const KVPlanes kv = kv_layout(proj, D, sh);
+        if (sh.Lk % 32 != 0) zero_floats(s, reinterpret_cast<float *>(kv.vt), 3 * kv.vt_stride / 2);
+        DBuf nq = obuf(s, B * Lq * D, P);
+        const Planes nqp = planes_in(nq, B * Lq * D, P);
+        layer_norm_planes(s, xq, (int)(B * Lq), D, L.n1w, L.n1b, nqp);
+        if (L.cross) {
+            DBuf nk = obuf(s, B * Lk * D, P);
+            const Planes nkp = planes_in(nk, B * Lk * D, P);
+            layer_norm_planes(s, xkv, (int)(B * Lk), D, L.n2w, L.n2b, nkp);
+            linear_planes(s, nqp, D, Lq * D, L.in_wp, L.in_b, B, (int)Lq, D, D, proj, Planes{}, D, Lq * D, TAIL_BIAS,
+                          nullptr, nullptr, nullptr);
+            linear_qkv_planes(s, nkp, D, Lk * D, L.in_wp.offset((int64_t)D * D), L.in_b + D, B, (int)Lk, D, 2 * D,
+                              0, nullptr, kv);
+        } else {
+            linear_qkv_planes(s, nqp, D, Lq * D, L.in_wp, L.in_b, B, (int)Lq, D, 3 * D, D, proj, kv);
+        }
+        a = AttentionArgs{proj,  D,     nullptr, D,       nullptr,   D,      nullptr, D,
+                          B,     heads, (int)Lq, (int)Lk, D / heads, Lq * D, Lk * D,  Lq * D};
+        a.kv = kv;
+    } else if (L.cross) {
         float *q = proj, *kv = proj + B * Lq * D;
         if (P) {
             DBuf nq = obuf(s, B * Lq * D, P), nk = obuf(s, B * Lk * D, P);

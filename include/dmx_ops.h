@@ -73,6 +73,20 @@ int dmx_op_attention(void *stream, const float *q, const float *k, const float *
 int dmx_op_attention_pair(void *stream, const float *q0, const float *k0, const float *v0, float *out0, int n_q0,
                           int n_k0, const float *q1, const float *k1, const float *v1, float *out1, int n_q1,
                           int n_k1, int batch, int heads, float scale);
+/* The three-plane attention's operands, for timing its kernel alone (no
+ * counterpart in the reference): dmx_op_kv_planes writes K and V of one
+ * problem (batch, n_k, heads * 64 floats each) as three bf16 planes, K into
+ * k_planes (3 * batch * n_k * heads * 64 elements) and V transposed per head
+ * into vt_planes (3 * batch * heads * 64 * ldvt elements, ldvt = n_k rounded
+ * up to a multiple of 32); dmx_op_attention_pair_planes is
+ * dmx_op_attention_pair over such planes, one kernel launch. Both enqueue
+ * only (no synchronisation). */
+int dmx_op_kv_planes(void *stream, const float *k, const float *v, int batch, int heads, int n_k,
+                     unsigned short *k_planes, unsigned short *vt_planes);
+int dmx_op_attention_pair_planes(void *stream, const float *q0, unsigned short *kp0, unsigned short *vtp0,
+                                 float *out0, int n_q0, int n_k0, const float *q1, unsigned short *kp1,
+                                 unsigned short *vtp1, float *out1, int n_q1, int n_k1, int batch, int heads,
+                                 float scale);
 int dmx_op_layer_norm(void *stream, const float *x, int rows, int dim, const float *w, const float *b, float *out);
 int dmx_op_group_norm(void *stream, const float *x, int b, int c, int inner, int groups, const float *w,
                       const float *bias, float *out);

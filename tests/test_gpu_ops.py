@@ -414,6 +414,36 @@ def test_plane_linear_is_fp32_accurate(lib, rows, k, n):
     assert errs[0] < 1e-2 * errs[1], errs
 
 
+@pytest.mark.parametrize("nk0,nk1", [(1344, 2688), (70, 333)])
+def test_attention_pair_on_kv_planes_matches_pair(lib, nk0, nk1):
+    """dmx_op_kv_planes + dmx_op_attention_pair_planes (the launch bench.py
+    times) give what dmx_op_attention_pair gives under the default precision,
+    bit for bit: the same kernel on the same planes."""
+    r = rng(nk0 + nk1)
+    batch, heads = 2, 2
+    D = heads * 64
+    nq0, nq1 = nk1, nk0
+    q0, q1 = (dev(r.uniform(-2, 2, (batch, n, D)).astype(np.float32)) for n in (nq0, nq1))
+    k0, v0 = (dev(r.uniform(-2, 2, (batch, nk0, D)).astype(np.float32)) for _ in range(2))
+    k1, v1 = (dev(r.uniform(-2, 2, (batch, nk1, D)).astype(np.float32)) for _ in range(2))
+    ref0, ref1 = torch.empty(batch, nq0, D, device="cuda"), torch.empty(batch, nq1, D, device="cuda")
+    assert lib.dmx_op_set_precision(0) == 0
+    call(lib, "dmx_op_attention_pair", stream(), ptr(q0), ptr(k0), ptr(v0), ptr(ref0), nq0, nk0, ptr(q1), ptr(k1),
+         ptr(v1), ptr(ref1), nq1, nk1, batch, heads, ctypes.c_float(0.125))
+    planes = []
+    for k, v, nk in ((k0, v0, nk0), (k1, v1, nk1)):
+        ldvt = (nk + 31) // 32 * 32
+        kp = torch.empty(3 * batch * nk * D, dtype=torch.int16, device="cuda")
+        vt = torch.empty(3 * batch * D * ldvt, dtype=torch.int16, device="cuda")
+        call(lib, "dmx_op_kv_planes", stream(), ptr(k), ptr(v), batch, heads, nk, ptr(kp), ptr(vt))
+        planes.append((kp, vt))
+    o0, o1 = torch.empty_like(ref0), torch.empty_like(ref1)
+    call(lib, "dmx_op_attention_pair_planes", stream(), ptr(q0), ptr(planes[0][0]), ptr(planes[0][1]), ptr(o0), nq0,
+         nk0, ptr(q1), ptr(planes[1][0]), ptr(planes[1][1]), ptr(o1), nq1, nk1, batch, heads, ctypes.c_float(0.125))
+    torch.cuda.synchronize()
+    assert torch.equal(o0, ref0) and torch.equal(o1, ref1)
+
+
 @pytest.mark.parametrize("nq,nk", [(2688, 1344), (1344, 2688), (300, 333)])
 def test_plane_attention_is_fp32_accurate(lib, nq, nk):
     """The three-plane attention keeps fp32 accuracy: against a float64
