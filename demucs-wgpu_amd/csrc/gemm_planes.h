@@ -109,6 +109,7 @@ template <int BM, int BN, int WAVES_M, int STAGES, int P, int BK, int NW, class 
 __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(DMX_PLANES_WPE))) void gemm_planes_kernel(
     int M, int N, int K, PlaneRows al, PlaneRows bl, EP ep) {
     static_assert(BK == 16 || BK == 32 || BK == 64, "k-tile of one, two or four MFMA k-groups");
+    static_assert(BK == 16 || (BK / 16) % 2 == 0, "an even number of k-groups per k-tile");
     constexpr int G = BK / 16;              // MFMA k-groups per k-tile
     constexpr int CH = BK / 8;              // 16-byte chunks per staged row
     constexpr int RPI = 64 / CH;            // rows per 1 KB DMA instruction
@@ -214,23 +215,53 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(DMX_PLA
         if (st < nk) issue(st, st * BK);
 
     if constexpr (G > 1) {
-        // G k-groups per k-tile: group g + 1's reads fly during group g's MFMAs.
+        // All STAGES buffers start filling at once. Iteration kt issues its
+        // groups' MFMAs with group g + 1's reads in flight during group g's.
+        // Once the second-to-last group's MFMAs are issued, the wave waits
+        // for the last group's reads and for tile kt + 1's DMA, meets the
+        // other waves at the barrier (after which every wave is done with
+        // tile kt's buffer, which then takes tile kt + STAGES), and starts
+        // reading tile kt + 1's first group: the barrier and those reads
+        // overlap the MFMAs in the pipe and the last group's.
+        static_assert(PER_WAVE * (STAGES - 1) < 64, "pipeline depth");
+        if (STAGES - 1 < nk) issue(STAGES - 1, (STAGES - 1) * BK);
+        if (nk >= STAGES)
+            wait_vmcnt<PER_WAVE * (STAGES - 1)>();
+        else
+            wait_vmcnt<0>();
+        __builtin_amdgcn_s_barrier();
+        floatx4 fa[2][P * TM], fb[2][P * TN];
+        read_group(lds, 0, fa[0], fb[0]);
+        lds_wait(fa[0], fb[0]);
+        read_group(lds, 1, fa[1], fb[1]);
         for (int kt = 0; kt < nk; ++kt) {
-            if (kt + STAGES - 2 < nk)
-                wait_vmcnt<PER_WAVE * (STAGES - 2)>();
-            else
-                wait_vmcnt<0>();
-            __builtin_amdgcn_s_barrier();
-            if (kt + STAGES - 1 < nk) issue((kt + STAGES - 1) % STAGES, (kt + STAGES - 1) * BK);
             const unsigned short *stage = lds + (kt % STAGES) * STAGE;
-            floatx4 fa[2][P * TM], fb[2][P * TN];
-            read_group(stage, 0, fa[0], fb[0]);
+            const unsigned short *next = lds + ((kt + 1) % STAGES) * STAGE;
 #pragma unroll
             for (int g = 0; g < G; ++g) {
-                lds_wait(fa[g & 1], fb[g & 1]);
-                if (g + 1 < G) read_group(stage, g + 1, fa[(g + 1) & 1], fb[(g + 1) & 1]);
                 pin_regs(fa[g & 1], fb[g & 1]);
                 mfma_group(fa[g & 1], fb[g & 1]);
+                __builtin_amdgcn_sched_barrier(0);
+                if (g < G - 2) {
+                    lds_wait(fa[(g + 1) & 1], fb[(g + 1) & 1]);
+                    read_group(stage, g + 2, fa[g & 1], fb[g & 1]);
+                } else if (g == G - 2) {
+                    lds_wait(fa[(g + 1) & 1], fb[(g + 1) & 1]);
+                    if (kt + 1 < nk) {
+                        if (kt + STAGES - 1 < nk)
+                            wait_vmcnt<PER_WAVE * (STAGES - 2)>();
+                        else
+                            wait_vmcnt<0>();
+                        __builtin_amdgcn_s_barrier();
+                        if (kt + STAGES < nk) issue(kt % STAGES, (kt + STAGES) * BK);
+                        read_group(next, 0, fa[g & 1], fb[g & 1]);
+                    }
+                } else if (kt + 1 < nk) {
+                    // Group 0 of tile kt + 1 went into the registers of group
+                    // G - 2 (G is even); group 1 takes this group's.
+                    lds_wait(fa[0], fb[0]);
+                    read_group(next, 1, fa[1], fb[1]);
+                }
                 __builtin_amdgcn_sched_barrier(0);
             }
         }

@@ -1237,7 +1237,7 @@ struct GroupMark {
 // a lane-0 group's forward where the next lane-1 group starts (see below).
 void separate_device(dmx_runner *const *nets, const float *bag_weights, int n_nets, const uint8_t *wanted,
                      const float *mix, int64_t samples, int sample_rate, const dmx_separate_options &o, float *stems,
-                     std::vector<GroupMark> &marks, size_t &total, int stagger_default = 1,
+                     std::vector<GroupMark> &marks, size_t &total, int stagger_default = 0,
                      const std::function<void(int64_t, int64_t)> &on_final = nullptr) {
     if (n_nets < 1 || !nets || !nets[0]) throw_error(DMX_ERR_ARGUMENT, "no network");
     dmx_runner &r0 = *nets[0];
@@ -1359,10 +1359,9 @@ void separate_device(dmx_runner *const *nets, const float *bag_weights, int n_ne
         // point of its forward (`stagger_default`): 1 = before the
         // transformer, 2 = after it, 10 + i = after encoder level i, 20 + i =
         // after frequency decoder level i, 30 + i = after transformer layer
-        // i; 0 = at once. With the stems staying in HBM the transformer's
-        // start is best: one group's memory-heavy encoders then overlap the
-        // other group's MFMA-heavy transformer rather than its encoders
-        // (+0.3 % on the 60 s separation against starting at once). When the
+        // i; 0 = at once. With the stems staying in HBM, starting at once is
+        // best (30.7 ms against 31.0 ms when starting at the transformer, on
+        // the 60 s separation with the plane linears and attention). When the
         // stems go back to the host, a later start lets the first group end
         // early enough for its readback to overlap the second group's work.
         // DMX_LANE_STAGGER overrides the point, for tuning.
@@ -1563,9 +1562,9 @@ int host_separation(dmx_runner *const *nets, const float *bag_weights, int32_t n
                 // The second lane's group starts after the first group's
                 // third transformer layer: the first group then ends early
                 // enough for its readback (66 MB of a 60 s mix's 85 MB of
-                // stems) to overlap the second group's work. Against the
-                // start at the transformer (dmx_separate_device's) the
-                // forwards take 1.3 % longer and the call 3.5 % less time.
+                // stems) to overlap the second group's work (33.6-34.0 ms
+                // per 60 s call, against 35.2-35.4 ms with the second lane
+                // starting at once, dmx_separate_device's schedule).
                 if (staged)
                     separate_device(nets, bag_weights, n_nets, stems_wanted, mix.f(), samples, sample_rate, o,
                                     stems.f(), marks, total, 32, on_final);
