@@ -443,8 +443,9 @@ def attention_roofline_record(args, attn_ms, attn_tflops, traffic, traffic_sourc
     bf16 matrix cores, so its achieved rate is 6x the fp32-equivalent rate,
     against the bf16 dense peak; the fp32-MFMA kernel's is the fp32 rate
     against the fp32 peak."""
+    launch = "dmx_op_attention_pair_planes" if planes_attention(args) else "dmx_op_attention_pair"
     shape = (f"sum of 4*B*Lq*Lk*512 flops over (Lq, Lk) = (2688, 1344) and (1344, 2688), B={args.batch_chunks}, "
-             f"both directions in one launch (dmx_op_attention_pair); avg {attn_ms:.3f} ms per launch")
+             f"both directions in one launch ({launch}); avg {attn_ms:.3f} ms per launch")
     if planes_attention(args):
         achieved = 6.0 * attn_tflops
         return {"bound": "mfma", "achieved": round(achieved, 2), "peak": BF16_MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
