@@ -2,6 +2,9 @@
 // the MFMA GEMM of gemm.h: implicit-GEMM convolutions (nothing im2col'd to
 // HBM), GLU-fused rewrites, transposed convolutions as per-phase GEMMs, the
 // fused DConv layer, channel mixers and the transformer linears.
+#include <cstdlib>
+#include <type_traits>
+
 #include "gemm.h"
 #include "gemm_planes.h"
 #include "ops.h"
@@ -729,57 +732,78 @@ struct EpLinear {
 #define DMX_GLU48_BN 128
 #endif
 
-template <bool GLU, bool BF16, class AL, class BL, class EP>
+// PREC (gemm_kernel's): the three-plane mode serves the tiles it measured
+// faster on (the 192- and 96-row tiles of the encoder convs, the GLU
+// rewrites and the transposed convs: 8-20 % per kernel on MI355X); the
+// narrow tiles (32 and 64 rows, whose MFMA work per loaded element is
+// small) and the DConv conv2 loader (GroupNorm + GELU on load, VALU-bound)
+// measured 5-70 % slower with it and stay on the fp32 matrix cores.
+template <bool GLU, int PREC, class AL, class BL, class EP>
 void gemm_pick(hipStream_t s, int M, int N, int K, int batches, const AL &al, const BL &bl, const EP &ep) {
+    constexpr int BIG = (PREC == 3 && std::is_same<BL, NormGeluQuads>::value) ? 0 : PREC;
+    constexpr int NARROW = PREC == 3 ? 0 : PREC;
     if constexpr (GLU) {
         // M = C output channels; a block covers BM / 2 of them.
         if (M % 96 == 0)
-            launch_gemm<192, DMX_GLU96_BN, 2, true, BF16>(s, M, N, K, batches, al, bl, ep);  // 2 x 48 channels
+            launch_gemm<192, DMX_GLU96_BN, 2, true, BIG>(s, M, N, K, batches, al, bl, ep);  // 2 x 48 channels
         else if (M == 48)
-            launch_gemm<96, DMX_GLU48_BN, 1, true, BF16>(s, M, N, K, batches, al, bl, ep);   // 1 x 48 channels
+            launch_gemm<96, DMX_GLU48_BN, 1, true, BIG>(s, M, N, K, batches, al, bl, ep);   // 1 x 48 channels
         else if (M > 32)
-            launch_gemm<128, 128, 2, true, BF16>(s, M, N, K, batches, al, bl, ep);  // 2 x 32 channels
+            launch_gemm<128, 128, 2, true, BIG>(s, M, N, K, batches, al, bl, ep);  // 2 x 32 channels
         else
-            launch_gemm<64, 128, 1, true, BF16>(s, M, N, K, batches, al, bl, ep);
+            launch_gemm<64, 128, 1, true, NARROW>(s, M, N, K, batches, al, bl, ep);
     } else {
 #ifdef DMX_BIG_BM  // tuning builds only: a larger tile for tall problems
         if (M >= DMX_BIG_BM)
-            launch_gemm<DMX_BIG_BM, DMX_BIG_BN, DMX_BIG_WM, false, BF16>(s, M, N, K, batches, al, bl, ep);
+            launch_gemm<DMX_BIG_BM, DMX_BIG_BN, DMX_BIG_WM, false, BIG>(s, M, N, K, batches, al, bl, ep);
         else
 #endif
         if (M % 96 == 0 && M >= 192 && M <= 768)  // channel counts 192, 384, 768: 96-row wave tiles
-            launch_gemm<192, 64, 2, false, BF16>(s, M, N, K, batches, al, bl, ep);
+            launch_gemm<192, 64, 2, false, BIG>(s, M, N, K, batches, al, bl, ep);
         else if (M == 96)
-            launch_gemm<96, 128, 1, false, BF16>(s, M, N, K, batches, al, bl, ep);
+            launch_gemm<96, 128, 1, false, BIG>(s, M, N, K, batches, al, bl, ep);
         else if (M >= 96)
-            launch_gemm<128, 128, 2, false, BF16>(s, M, N, K, batches, al, bl, ep);
+            launch_gemm<128, 128, 2, false, BIG>(s, M, N, K, batches, al, bl, ep);
         else if (M > 32) {
             // 64-row tiles: 64-wide columns when 128-wide ones would leave CUs idle.
             if (ceil_div(N, 128) * ceil_div(M, 64) * batches < 256)
-                launch_gemm<64, 64, 2, false, BF16>(s, M, N, K, batches, al, bl, ep);
+                launch_gemm<64, 64, 2, false, NARROW>(s, M, N, K, batches, al, bl, ep);
             else
-                launch_gemm<64, 128, 2, false, BF16>(s, M, N, K, batches, al, bl, ep);
+                launch_gemm<64, 128, 2, false, NARROW>(s, M, N, K, batches, al, bl, ep);
         } else {
             // 32-row tiles: 128-wide columns unless 256-wide ones fill two rounds
             // of the CUs with little padding (short rows such as T = 336 pad a
             // 256-wide tile by a third).
             const int64_t n256 = ceil_div(N, 256) * 256;
             if (ceil_div(N, 256) * batches >= 512 && 5 * n256 <= 6 * (int64_t)N)
-                launch_gemm<32, 256, 1, false, BF16>(s, M, N, K, batches, al, bl, ep);
+                launch_gemm<32, 256, 1, false, NARROW>(s, M, N, K, batches, al, bl, ep);
             else
-                launch_gemm<32, 128, 1, false, BF16>(s, M, N, K, batches, al, bl, ep);
+                launch_gemm<32, 128, 1, false, NARROW>(s, M, N, K, batches, al, bl, ep);
         }
     }
 }
 
-// Contractions take bf16 MFMA inputs when the calling thread's precision
-// scope says so (fp32 accumulation and epilogues either way).
+// The fp32 precision's convolutions run on three bf16 planes per operand
+// unless DMX_CONV_PLANES=0 (read once) keeps them on the fp32 matrix cores.
+bool conv_planes_enabled() {
+    static const bool on = [] {
+        const char *e = std::getenv("DMX_CONV_PLANES");
+        return !e || std::atoi(e) != 0;
+    }();
+    return on;
+}
+
+// Contractions take bf16 MFMA inputs, or three bf16 planes, when the calling
+// thread's precision scope says so (fp32 accumulation and epilogues either
+// way).
 template <bool GLU, class AL, class BL, class EP>
 void gemm_auto(hipStream_t s, int M, int N, int K, int batches, const AL &al, const BL &bl, const EP &ep) {
     if (bf16_mfma())
-        gemm_pick<GLU, true>(s, M, N, K, batches, al, bl, ep);
+        gemm_pick<GLU, 1>(s, M, N, K, batches, al, bl, ep);
+    else if (mfma_precision() == MfmaPrecision::FP32X3 && conv_planes_enabled())
+        gemm_pick<GLU, 3>(s, M, N, K, batches, al, bl, ep);
     else
-        gemm_pick<GLU, false>(s, M, N, K, batches, al, bl, ep);
+        gemm_pick<GLU, 0>(s, M, N, K, batches, al, bl, ep);
 }
 
 bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }

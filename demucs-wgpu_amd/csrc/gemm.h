@@ -64,18 +64,44 @@ __device__ __forceinline__ uint2 pack_bf16x4(float4 v) {
     return make_uint2(__builtin_bit_cast(unsigned, lo), __builtin_bit_cast(unsigned, hi));
 }
 
-// Stage element type and depth: fp32 stages BK = 16 floats per row; bf16
-// stages 32 (one v_mfma_f32_32x32x16_bf16 per 16, operands 8 bf16 per lane).
-template <bool BF16>
+// MFMA input precision of gemm_kernel (its PREC parameter): fp32 (0), bf16
+// (1), or three bf16 planes per operand (3: x = x0 + x1 + x2, the six plane
+// products with i + j < 3 summed in fp32, an fp32-accurate product; the
+// loader splits each value into its planes as it stores it in LDS).
+// Stage element type, depth and planes: fp32 stages BK = 16 floats per row;
+// bf16 stages 32 (one v_mfma_f32_32x32x16_bf16 per 16, operands 8 bf16 per
+// lane); three planes stage 16 per plane.
+template <int PREC>
 struct GemmStage {
     using T = float;
     static constexpr int BK = GEMM_BK;
+    static constexpr int PLANES = 1;
 };
 template <>
-struct GemmStage<true> {
+struct GemmStage<1> {
     using T = unsigned short;
     static constexpr int BK = 32;
+    static constexpr int PLANES = 1;
 };
+template <>
+struct GemmStage<3> {
+    using T = unsigned short;
+    static constexpr int BK = 16;
+    static constexpr int PLANES = 3;
+};
+
+// Four values -> three bf16 planes (round to nearest even at each step), as
+// bits, four per uint2.
+__device__ __forceinline__ void split_planes4(float4 v, uint2 (&out)[3]) {
+    float r[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+    for (int q = 0; q < 3; ++q) {
+        unsigned short h[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) h[e] = bf16_split_step(r[e]);
+        out[q] = make_uint2((unsigned)h[0] | ((unsigned)h[1] << 16), (unsigned)h[2] | ((unsigned)h[3] << 16));
+    }
+}
 
 // An m/n-major loader may fetch four consecutive k of one column at once
 // (load_quad, k a multiple of 4); when K is a multiple of 4 a quad is either
@@ -130,10 +156,11 @@ __device__ __forceinline__ void block_tile(int &bx, int &by, int &z) {
     z = lb / (nx * ny);
 }
 
-template <int BM, int BN, int WAVES_M, bool GLU, bool BF16, class AL, class BL, class EP>
+template <int BM, int BN, int WAVES_M, bool GLU, int PREC, class AL, class BL, class EP>
 __global__ __launch_bounds__(GEMM_THREADS) void gemm_kernel(int M, int N, int K, AL al, BL bl, EP ep) {
-    using T = typename GemmStage<BF16>::T;
-    constexpr int BK = GemmStage<BF16>::BK;
+    using T = typename GemmStage<PREC>::T;
+    constexpr int BK = GemmStage<PREC>::BK;
+    constexpr int NP = GemmStage<PREC>::PLANES;
     constexpr int KQ = BK / 4;                  // 4-k chunks per row of a stage
     constexpr int LD = BK + 16 / (int)sizeof(T);  // LDS row stride: 16 bytes of padding
     static_assert(BK % 8 == 0, "BK must be a multiple of 8");
@@ -143,8 +170,8 @@ __global__ __launch_bounds__(GEMM_THREADS) void gemm_kernel(int M, int N, int K,
     static_assert(TM >= 1 && TN >= 1, "wave tile must hold at least one 32x32 MFMA tile");
     static_assert(!GLU || TM == 2 || TM == 3, "GLU waves hold 32 or 48 channels (value + gate tiles)");
     constexpr int GCH = WTM / 2;  // GLU channels per wave
-    __shared__ __align__(16) T As[2][BM][LD];
-    __shared__ __align__(16) T Bs[2][BN][LD];
+    __shared__ __align__(16) T As[2][NP][BM][LD];
+    __shared__ __align__(16) T Bs[2][NP][BN][LD];
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int wm = wave % WAVES_M, wn = wave / WAVES_M;
@@ -247,26 +274,35 @@ __global__ __launch_bounds__(GEMM_THREADS) void gemm_kernel(int M, int N, int K,
         else
             load_tiles(k0, std::false_type{});
     };
-    auto put = [&](T *dst, const float4 &v) {
-        if constexpr (BF16)
+    // Four values of row r, k-quad q into LDS (plane stride PS elements).
+    auto put = [&](T *dst, int64_t ps, const float4 &v) {
+        if constexpr (PREC == 3) {
+            uint2 pl[3];
+            split_planes4(v, pl);
+#pragma unroll
+            for (int q = 0; q < 3; ++q) *reinterpret_cast<uint2 *>(dst + q * ps) = pl[q];
+        } else if constexpr (PREC == 1) {
+            (void)ps;
             *reinterpret_cast<uint2 *>(dst) = pack_bf16x4(v);
-        else
+        } else {
+            (void)ps;
             *reinterpret_cast<float4 *>(dst) = v;
+        }
     };
     auto store_tiles = [&](int buf, int k0) {
 #pragma unroll
         for (int it = 0; it < A_ITEMS; ++it) {
             int e = tid + it * GEMM_THREADS;
-            if (e < BM * KQ) put(&As[buf][a_row(e)][4 * a_quad(e)], areg[it]);
+            if (e < BM * KQ) put(&As[buf][0][a_row(e)][4 * a_quad(e)], BM * LD, areg[it]);
         }
 #pragma unroll
         for (int it = 0; it < B_ITEMS; ++it) {
             int e = tid + it * GEMM_THREADS;
             if (e < BN * KQ) {
                 if constexpr (B_RAW)
-                    put(&Bs[buf][b_row(e)][4 * b_quad(e)], bl.finish(bst[it], breg[it], k0 + 4 * b_quad(e)));
+                    put(&Bs[buf][0][b_row(e)][4 * b_quad(e)], BN * LD, bl.finish(bst[it], breg[it], k0 + 4 * b_quad(e)));
                 else
-                    put(&Bs[buf][b_row(e)][4 * b_quad(e)], breg[it]);
+                    put(&Bs[buf][0][b_row(e)][4 * b_quad(e)], BN * LD, breg[it]);
             }
         }
     };
@@ -290,17 +326,45 @@ __global__ __launch_bounds__(GEMM_THREADS) void gemm_kernel(int M, int N, int K,
 #ifdef DMX_GEMM_SETPRIO  // tuning builds only
         __builtin_amdgcn_s_setprio(1);
 #endif
-        if constexpr (BF16) {
+        if constexpr (PREC == 3) {
+            // Three planes: lane half h holds k = 16g + 8h .. +7 of its row in
+            // every plane; the six plane products with i + j < 3, smallest
+            // first.
+#pragma unroll
+            for (int g = 0; g < BK / 16; ++g) {
+                bf16x8 a[3][TM], b[3][TN];
+#pragma unroll
+                for (int q = 0; q < 3; ++q) {
+#pragma unroll
+                    for (int i = 0; i < TM; ++i)
+                        a[q][i] = *reinterpret_cast<const bf16x8 *>(
+                            &As[cur][q][wm * WTM + i * 32 + row_in][16 * g + 8 * khalf]);
+#pragma unroll
+                    for (int j = 0; j < TN; ++j)
+                        b[q][j] = *reinterpret_cast<const bf16x8 *>(
+                            &Bs[cur][q][wn * WTN + j * 32 + row_in][16 * g + 8 * khalf]);
+                }
+                constexpr int pa[6] = {2, 1, 0, 1, 0, 0}, pb[6] = {0, 1, 2, 0, 1, 0};
+#pragma unroll
+                for (int t = 0; t < 6; ++t)
+#pragma unroll
+                    for (int i = 0; i < TM; ++i)
+#pragma unroll
+                        for (int j = 0; j < TN; ++j)
+                            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[pa[t]][i], b[pb[t]][j], acc[i][j],
+                                                                                0, 0, 0);
+            }
+        } else if constexpr (PREC == 1) {
             // Lane half h holds k = 16g + 8h .. +7 of its row for A and B alike.
 #pragma unroll
             for (int g = 0; g < BK / 16; ++g) {
                 bf16x8 a[TM], b[TN];
 #pragma unroll
                 for (int i = 0; i < TM; ++i)
-                    a[i] = *reinterpret_cast<const bf16x8 *>(&As[cur][wm * WTM + i * 32 + row_in][16 * g + 8 * khalf]);
+                    a[i] = *reinterpret_cast<const bf16x8 *>(&As[cur][0][wm * WTM + i * 32 + row_in][16 * g + 8 * khalf]);
 #pragma unroll
                 for (int j = 0; j < TN; ++j)
-                    b[j] = *reinterpret_cast<const bf16x8 *>(&Bs[cur][wn * WTN + j * 32 + row_in][16 * g + 8 * khalf]);
+                    b[j] = *reinterpret_cast<const bf16x8 *>(&Bs[cur][0][wn * WTN + j * 32 + row_in][16 * g + 8 * khalf]);
 #pragma unroll
                 for (int i = 0; i < TM; ++i)
 #pragma unroll
@@ -313,10 +377,10 @@ __global__ __launch_bounds__(GEMM_THREADS) void gemm_kernel(int M, int N, int K,
                 floatx4 a[TM], b[TN];
 #pragma unroll
                 for (int i = 0; i < TM; ++i)
-                    a[i] = *reinterpret_cast<const floatx4 *>(&As[cur][wm * WTM + i * 32 + row_in][8 * g + 4 * khalf]);
+                    a[i] = *reinterpret_cast<const floatx4 *>(&As[cur][0][wm * WTM + i * 32 + row_in][8 * g + 4 * khalf]);
 #pragma unroll
                 for (int j = 0; j < TN; ++j)
-                    b[j] = *reinterpret_cast<const floatx4 *>(&Bs[cur][wn * WTN + j * 32 + row_in][8 * g + 4 * khalf]);
+                    b[j] = *reinterpret_cast<const floatx4 *>(&Bs[cur][0][wn * WTN + j * 32 + row_in][8 * g + 4 * khalf]);
 #pragma unroll
                 for (int t = 0; t < 4; ++t)
 #pragma unroll
@@ -382,13 +446,13 @@ __global__ __launch_bounds__(GEMM_THREADS) void gemm_kernel(int M, int N, int K,
 }
 
 // Launches gemm_kernel on `stream` for `batches` independent problems.
-template <int BM, int BN, int WAVES_M, bool GLU, bool BF16 = false, class AL, class BL, class EP>
+template <int BM, int BN, int WAVES_M, bool GLU, int PREC = 0, class AL, class BL, class EP>
 void launch_gemm(hipStream_t stream, int M, int N, int K, int batches, const AL &al, const BL &bl, const EP &ep) {
     if (M <= 0 || N <= 0 || batches <= 0) return;
     const int m_per_block = GLU ? BM / 2 : BM;
     dim3 grid((unsigned)ceil_div(N, BN), (unsigned)ceil_div(M, m_per_block), (unsigned)batches);
     DMX_REQUIRE(grid.y <= 65535 && grid.z <= 65535, "GEMM grid too large");
-    hipLaunchKernelGGL((gemm_kernel<BM, BN, WAVES_M, GLU, BF16, AL, BL, EP>), grid, dim3(GEMM_THREADS), 0, stream, M,
+    hipLaunchKernelGGL((gemm_kernel<BM, BN, WAVES_M, GLU, PREC, AL, BL, EP>), grid, dim3(GEMM_THREADS), 0, stream, M,
                        N, K, al, bl, ep);
     DMX_LAUNCH_CHECK();
 }

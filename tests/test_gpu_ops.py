@@ -31,6 +31,16 @@ def stream():
     return ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
 
 
+@pytest.fixture(params=[0, 2], ids=["fp32_planes", "fp32_mfma"])
+def fp32_precision(lib, request):
+    """Both fp32 settings of dmx_op_set_precision: the default (linears,
+    attention and the wide-tile convolutions on three bf16 planes per
+    operand) and fp32 MFMA everywhere."""
+    assert lib.dmx_op_set_precision(request.param) == 0
+    yield request.param
+    assert lib.dmx_op_set_precision(0) == 0
+
+
 @pytest.fixture(scope="module")
 def lib(dmx):
     from demucs_wgpu_amd import _native
@@ -42,15 +52,6 @@ def call(lib, name, *args):
     torch.cuda.synchronize()
     if rc != 0:
         raise RuntimeError(f"{name}: {lib.dmx_last_error().decode()}")
-
-
-@pytest.fixture(params=[0, 2], ids=["fp32_planes", "fp32_mfma"])
-def fp32_precision(lib, request):
-    """Both fp32 settings of dmx_op_set_precision: the default (linears on
-    three bf16 planes per operand) and fp32 MFMA everywhere."""
-    assert lib.dmx_op_set_precision(request.param) == 0
-    yield request.param
-    assert lib.dmx_op_set_precision(0) == 0
 
 
 @pytest.mark.parametrize("rows,k,n,tail", [(300, 512, 1536, 0), (37, 19, 70, 0), (64, 512, 2048, 1),
@@ -81,7 +82,7 @@ def test_linear_matches_oracle(lib, oracle, fp32_precision, rows, k, n, tail):
     (1, 5, 7, 13, 130, 1, 1, 1, 1, 0, 0, 1, 1),     # 1x1, M > 128 (two m-tiles)
     (1, 3, 9, 10, 7, 2, 3, 2, 3, 1, 2, 2, 1),       # generic kernel path
 ])
-def test_conv2d_matches_oracle(lib, oracle, b, ic, h, w, oc, kh, kw, sh, sw, ph, pw, dh, dw):
+def test_conv2d_matches_oracle(lib, oracle, fp32_precision, b, ic, h, w, oc, kh, kw, sh, sw, ph, pw, dh, dw):
     r = rng(ic * 31 + oc)
     x = r.uniform(-0.4, 0.4, (b, ic, h, w)).astype(np.float32)
     wt = r.uniform(-0.4, 0.4, (oc, ic, kh, kw)).astype(np.float32)
@@ -110,7 +111,7 @@ def test_conv2d_gelu_and_skip(lib, oracle):
 
 @pytest.mark.parametrize("b,ic,h,w,C,kh,kw", [(1, 48, 32, 12, 48, 1, 1), (2, 24, 1, 300, 24, 1, 3),
                                                (1, 16, 10, 9, 16, 3, 3), (1, 96, 4, 7, 96, 1, 1)])
-def test_conv2d_glu_matches_oracle(lib, oracle, b, ic, h, w, C, kh, kw):
+def test_conv2d_glu_matches_oracle(lib, oracle, fp32_precision, b, ic, h, w, C, kh, kw):
     r = rng(C + kh)
     x = r.uniform(-0.4, 0.4, (b, ic, h, w)).astype(np.float32)
     wt = r.uniform(-0.4, 0.4, (2 * C, ic, kh, kw)).astype(np.float32)
@@ -162,7 +163,7 @@ def test_conv2d_glu_adds_the_frequency_embedding(lib, oracle):
 
 @pytest.mark.parametrize("b,ic,A,P,oc,last", [(1, 48, 32, 11, 16, True), (2, 96, 8, 5, 48, False),
                                               (1, 48, 301, 1, 8, True), (2, 24, 50, 1, 12, False)])
-def test_conv_transpose_matches_oracle(lib, oracle, b, ic, A, P, oc, last):
+def test_conv_transpose_matches_oracle(lib, oracle, fp32_precision, b, ic, A, P, oc, last):
     r = rng(ic + A)
     x = r.uniform(-0.4, 0.4, (b, ic, A, P)).astype(np.float32)
     wt = r.uniform(-0.4, 0.4, (ic, oc, 8, 1)).astype(np.float32)
@@ -212,7 +213,7 @@ def dconv_reference(oracle, x, w):
 @pytest.mark.parametrize("B,C,F,T", [(1, 48, 16, 40), (2, 96, 1, 700), (1, 384, 2, 33), (2, 192, 3, 300),
                                      (1, 48, 1, 1000), (2, 48, 3, 77), (1, 96, 5, 65), (1, 96, 2, 336),
                                      (1, 192, 1, 1500), (1, 384, 2, 336)])
-def test_dconv_matches_oracle(lib, oracle, dmx, B, C, F, T):
+def test_dconv_matches_oracle(lib, oracle, fp32_precision, dmx, B, C, F, T):
     hid, w, x = dconv_case(C, C + T, B, F, T)
     ref = dconv_reference(oracle, x, w)
     dx = dev(x)
