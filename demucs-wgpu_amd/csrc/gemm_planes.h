@@ -16,11 +16,13 @@
 // on MI355X (2.5 PFLOP/s dense bf16 / 6 against 157.3 TFLOP/s fp32).
 // P = 1 is a plain bf16 GEMM (bf16 inputs, fp32 accumulation).
 //
-// The kernel is the direct-to-LDS design of gemm_dma_kernel (gemm.h) with
-// 64-byte rows of 32 bf16 per k-tile: global_load_lds_dwordx4 fills LDS with
-// no staging registers, STAGES k-tiles in flight, the same XOR swizzle of the
-// four 16-byte chunks of a row, one barrier per k-tile. A stage holds the P
-// planes of the A rows, then the P planes of the B rows.
+// The kernel is the direct-to-LDS design of gemm_dma_kernel (gemm.h) over
+// rows of 16, 32 or 64 bf16 per k-tile (one, two or four MFMA k-groups):
+// global_load_lds_dwordx4 fills LDS with no staging registers, STAGES k-tiles
+// in flight, an XOR swizzle of a row's 16-byte chunks keeps the operand reads
+// conflict-free, and one barrier per k-tile sits between the last two
+// k-groups' MFMAs. A stage holds the P planes of the A rows, then the P
+// planes of the B rows. Four or eight waves per workgroup.
 #pragma once
 
 #include "gemm.h"
