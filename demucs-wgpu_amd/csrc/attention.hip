@@ -587,24 +587,62 @@ __global__ __launch_bounds__(256) void attention_bf16_kernel(const AttGroup g) {
 // operand is one 16-byte LDS read and staging is plain 16-byte copies.
 // Key tiles are 32 keys, double buffered: the three planes of a K tile and a
 // V^T tile take 54 KB, so two workgroups (two waves per SIMD) share a CU.
+// Software pipeline: while a wave turns tile t's scores into probabilities
+// (exponentials, row sums, plane splits: VALU work) it issues the 24 score
+// MFMAs of tile t + 1 between those instructions, so the VALU work runs in
+// the matrix core's busy cycles; then come tile t's 24 P V MFMAs. The K
+// buffers run one tile ahead of the V^T buffers, and one barrier per tile
+// covers both.
 // ---------------------------------------------------------------------------
 
 constexpr int AX_KT = 32;   // keys per tile
 constexpr int AX_LDK = 72;  // bf16 per K row (144 B: conflict-free b128 reads)
 constexpr int AX_LDV = 40;  // bf16 per V^T row (80 B: conflict-free b128 reads)
 
-// Three bf16 planes of eight fp32 values (round to nearest even at each
-// step). The residual of each step comes from the packed bf16 pair itself
-// (low half << 16, high half & 0xffff0000), one conversion per two values.
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+
+// max / sum of x over a lane pair (l, l + 32), one v_permlane32_swap: the
+// swap leaves the lower lane's value in one register and the upper lane's
+// in the other on both lanes, so both get the same bits. Inline asm: the
+// compiler's builtin for this instruction returned the first register for
+// both results. The nops cover the VALU-write -> permlane-read and
+// permlane-write -> VALU-read dependencies.
+__device__ __forceinline__ void att_swap_halves(float x, float &a, float &b) {
+    unsigned u = __builtin_bit_cast(unsigned, x), w = u;
+    asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1\n\ts_nop 1" : "+v"(u), "+v"(w));
+    a = __builtin_bit_cast(float, u);
+    b = __builtin_bit_cast(float, w);
+}
+__device__ __forceinline__ float att_pair_max(float x) {
+    float a, b;
+    att_swap_halves(x, a, b);
+    return fmaxf(a, b);
+}
+__device__ __forceinline__ float att_pair_sum(float x) {
+    float a, b;
+    att_swap_halves(x, a, b);
+    return a + b;
+}
+
+// Three bf16 planes of fp32 values, round to nearest even at each step:
+// a plane pair h = (bf16(x0), bf16(x1)) is one v_cvt_pk_bf16_f32, and the
+// residuals x - plane (exact in fp32) take the planes' bits straight from
+// the packed pair (low half << 16, high half & 0xffff0000).
+__device__ __forceinline__ void att_residual(bf16x2 h, float &x0, float &x1) {
+    const unsigned u = __builtin_bit_cast(unsigned, h);
+    x0 -= __builtin_bit_cast(float, u << 16);
+    x1 -= __builtin_bit_cast(float, u & 0xffff0000u);
+}
+
 __device__ __forceinline__ void split3(floatx8 x, bf16x8 &p0, bf16x8 &p1, bf16x8 &p2) {
-    typedef unsigned uintx4 __attribute__((ext_vector_type(4)));
     auto step = [](floatx8 &v) {
         const bf16x8 h = __builtin_convertvector(v, bf16x8);
-        const uintx4 u = __builtin_bit_cast(uintx4, h);
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-            v[2 * e] -= __builtin_bit_cast(float, u[e] << 16);
-            v[2 * e + 1] -= __builtin_bit_cast(float, u[e] & 0xffff0000u);
+            float x0 = v[2 * e], x1 = v[2 * e + 1];
+            att_residual((bf16x2){h[2 * e], h[2 * e + 1]}, x0, x1);
+            v[2 * e] = x0;
+            v[2 * e + 1] = x1;
         }
         return h;
     };
@@ -658,141 +696,251 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void a
     const uint32_t vofs = (uint32_t)(((tid >> 2) * P_.ldvt + 8 * (tid & 3)) * sizeof(unsigned short));
     const uint32_t kbytes = (uint32_t)(((int64_t)(n_k - 1) * kld + ATT_D) * sizeof(unsigned short));
     floatx4 kpre[3], vpre[3];
-    auto fetch = [&](int key0) {
+    auto fetch_k = [&](int key0) {
 #pragma unroll
         for (int pl = 0; pl < 3; ++pl) {
             const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(
                 const_cast<unsigned short *>(kpb + pl * P_.kp_ps + (int64_t)key0 * kld), (short)0,
                 (int)(kbytes - (uint32_t)(key0 * kld * sizeof(unsigned short))), 0x00020000);
             kpre[pl] = __builtin_bit_cast(floatx4, __builtin_amdgcn_raw_buffer_load_b128(rk, kofs, 0, 0));
-            vpre[pl] = *reinterpret_cast<const floatx4 *>(
-                reinterpret_cast<const char *>(vtb + pl * P_.vt_ps + key0) + vofs);
         }
     };
-    auto stage = [&](int buf) {
+    auto fetch_v = [&](int key0) {
 #pragma unroll
-        for (int pl = 0; pl < 3; ++pl) {
+        for (int pl = 0; pl < 3; ++pl)
+            vpre[pl] = *reinterpret_cast<const floatx4 *>(reinterpret_cast<const char *>(vtb + pl * P_.vt_ps + key0) +
+                                                          vofs);
+    };
+    auto stage_k = [&](int buf) {
+#pragma unroll
+        for (int pl = 0; pl < 3; ++pl)
             *reinterpret_cast<floatx4 *>(&Ks[buf][pl][tid >> 3][8 * (tid & 7)]) = kpre[pl];
+    };
+    auto stage_v = [&](int buf) {
+#pragma unroll
+        for (int pl = 0; pl < 3; ++pl)
             *reinterpret_cast<floatx4 *>(&Vt[buf][pl][tid >> 2][8 * (tid & 3)]) = vpre[pl];
-        }
     };
 
+    // Scores stay raw (log2 units); mb is the offset of the exponentials,
+    // exp2(s - mb), raised lazily: only when some query's tile max exceeds
+    // lim = mb + ATT_SLACK (always on the first tile, lim = -inf).
     const floatx16 zero = {};
     floatx16 o0 = zero, o1 = zero;
-    float m_run = -INFINITY, l_run = 0.0f;
-    floatx16 negmb = zero;
-    float mb = 0.0f, thr = -INFINITY;
+    float mb = -INFINITY, lim = -INFINITY, l_run = 0.0f;
 
-    // One 32-key tile; MASK only for a ragged last tile. Register r of the
-    // scores holds key key0 + 8(r/4) + 4*half + r%4.
-    auto tile = [&](auto mask_tag, int buf, int key0) {
-        constexpr bool MASK = decltype(mask_tag)::value;
-        floatx16 sc = negmb;
-        att_prio(1);
+    // Score MFMA i of k-group t4 of the tile whose K fragments are kf, onto
+    // acc; smallest products first.
+    auto score_mfma = [&](int t4, int i, const bf16x8 (&kf)[3], floatx16 acc) {
+        constexpr int ka[6] = {2, 1, 0, 1, 0, 0}, qa[6] = {0, 1, 2, 0, 1, 0};
+        return __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[ka[i]], qf[qa[i]][t4], acc, 0, 0, 0);
+    };
+    auto read_k = [&](int buf, int t4, bf16x8 (&kf)[3]) {
 #pragma unroll
-        for (int t = 0; t < 4; ++t) {
+        for (int pl = 0; pl < 3; ++pl) kf[pl] = *reinterpret_cast<const bf16x8 *>(&Ks[buf][pl][j][16 * t4 + 8 * half]);
+    };
+    // Scores of the tile in K buffer buf: register r holds key 8(r/4) +
+    // 4*half + r%4 of the tile.
+    auto scores = [&](int buf) {
+        floatx16 sc = zero;
+#pragma unroll
+        for (int t4 = 0; t4 < 4; ++t4) {
             bf16x8 kf[3];
+            read_k(buf, t4, kf);
 #pragma unroll
-            for (int pl = 0; pl < 3; ++pl)
-                kf[pl] = *reinterpret_cast<const bf16x8 *>(&Ks[buf][pl][j][16 * t + 8 * half]);
-            // Smallest products first.
-            sc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[2], qf[0][t], sc, 0, 0, 0);
-            sc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[1], qf[1][t], sc, 0, 0, 0);
-            sc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[0], qf[2][t], sc, 0, 0, 0);
-            sc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[1], qf[0][t], sc, 0, 0, 0);
-            sc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[0], qf[1][t], sc, 0, 0, 0);
-            sc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[0], qf[0][t], sc, 0, 0, 0);
+            for (int i = 0; i < 6; ++i) sc = score_mfma(t4, i, kf, sc);
         }
-        if constexpr (MASK) {
-#pragma unroll
-            for (int r = 0; r < 16; ++r)
-                if (key0 + 8 * (r >> 2) + 4 * half + (r & 3) >= n_k) sc[r] = -INFINITY;
-        }
-        att_prio(0);
+        return sc;
+    };
+    auto row_max = [&](const floatx16 &sc) {
         float mloc = sc[0];
 #pragma unroll
         for (int r = 1; r < 16; ++r) mloc = fmaxf(mloc, sc[r]);
-        mloc = fmaxf(mloc, __shfl_xor(mloc, 32, 64));
-        if (__any(mloc > thr)) {
-            const float m_new = fmaxf(m_run, mloc + mb);
-            const float corr = __builtin_amdgcn_exp2f(m_run - m_new);
-            const float shift = m_new - mb;
+        return att_pair_max(mloc);
+    };
+    // Raises mb to the running max when some query's tile max mloc exceeds
+    // lim, rescaling O and the row sum (O and the sum carry the same factor,
+    // which the final division cancels).
+    auto raise_max = [&](float mloc) {
+        if (__any(mloc > lim)) {
+            const float m_new = fmaxf(mb, mloc);
+            const float corr = __builtin_amdgcn_exp2f(mb - m_new);
             l_run *= corr;
-            m_run = m_new;
             mb = m_new;
-            thr = ATT_SLACK;
+            lim = m_new + ATT_SLACK;
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
                 o0[r] *= corr;
                 o1[r] *= corr;
-                sc[r] -= shift;
-                negmb[r] = -m_new;
             }
         }
-        float lsum = 0.0f;
+    };
+    // P's planes in the B-operand order: registers 8m .. 8m+7 are keys
+    // 16m + 4*half + 0..3 and 16m + 8 + 4*half + 0..3, which V^T stores
+    // contiguously at 16m + 8*half. Plane word pw[q][m][e] holds registers
+    // 8m + 2e and 8m + 2e + 1.
+    typedef unsigned uintx4 __attribute__((ext_vector_type(4)));
+    auto split_pair = [&](const floatx16 &p, int u, uintx4 (&pw)[3][2]) {
+        const int m = u / 4, e = u % 4;
+        float x0 = p[2 * u], x1 = p[2 * u + 1];
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-            sc[r] = __builtin_amdgcn_exp2f(sc[r]);
-            lsum += sc[r];
+        for (int q = 0; q < 2; ++q) {
+            const bf16x2 h = {(__bf16)x0, (__bf16)x1};
+            pw[q][m][e] = __builtin_bit_cast(unsigned, h);
+            att_residual(h, x0, x1);
         }
-        lsum += __shfl_xor(lsum, 32, 64);
-        l_run += lsum;
-        // P planes in the B-operand order: registers 8m .. 8m+7 are keys
-        // 16m + 4*half + 0..3 and 16m + 8 + 4*half + 0..3, which V^T stores
-        // contiguously at 16m + 8*half.
-        bf16x8 pp[3][2];
+        const bf16x2 h = {(__bf16)x0, (__bf16)x1};
+        pw[2][m][e] = __builtin_bit_cast(unsigned, h);
+    };
+    auto planes_of = [&](const uintx4 (&pw)[3][2], bf16x8 (&pp)[3][2]) {
 #pragma unroll
-        for (int m = 0; m < 2; ++m)
-            split3((floatx8){sc[8 * m], sc[8 * m + 1], sc[8 * m + 2], sc[8 * m + 3], sc[8 * m + 4], sc[8 * m + 5],
-                             sc[8 * m + 6], sc[8 * m + 7]},
-                   pp[0][m], pp[1][m], pp[2][m]);
-        att_prio(1);
+        for (int q = 0; q < 3; ++q)
 #pragma unroll
-        for (int m = 0; m < 2; ++m) {
-            bf16x8 va[3], vc[3];
+            for (int m = 0; m < 2; ++m) pp[q][m] = __builtin_bit_cast(bf16x8, pw[q][m]);
+    };
+    auto read_v = [&](int buf, int m, bf16x8 (&va)[3], bf16x8 (&vc)[3]) {
 #pragma unroll
-            for (int pl = 0; pl < 3; ++pl) {
-                va[pl] = *reinterpret_cast<const bf16x8 *>(&Vt[buf][pl][j][16 * m + 8 * half]);
-                vc[pl] = *reinterpret_cast<const bf16x8 *>(&Vt[buf][pl][32 + j][16 * m + 8 * half]);
-            }
-            o0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(va[2], pp[0][m], o0, 0, 0, 0);
-            o1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vc[2], pp[0][m], o1, 0, 0, 0);
-            o0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(va[1], pp[1][m], o0, 0, 0, 0);
-            o1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vc[1], pp[1][m], o1, 0, 0, 0);
-            o0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(va[0], pp[2][m], o0, 0, 0, 0);
-            o1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vc[0], pp[2][m], o1, 0, 0, 0);
-            o0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(va[1], pp[0][m], o0, 0, 0, 0);
-            o1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vc[1], pp[0][m], o1, 0, 0, 0);
-            o0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(va[0], pp[1][m], o0, 0, 0, 0);
-            o1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vc[0], pp[1][m], o1, 0, 0, 0);
-            o0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(va[0], pp[0][m], o0, 0, 0, 0);
-            o1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vc[0], pp[0][m], o1, 0, 0, 0);
+        for (int pl = 0; pl < 3; ++pl) {
+            va[pl] = *reinterpret_cast<const bf16x8 *>(&Vt[buf][pl][j][16 * m + 8 * half]);
+            vc[pl] = *reinterpret_cast<const bf16x8 *>(&Vt[buf][pl][32 + j][16 * m + 8 * half]);
         }
-        att_prio(0);
+    };
+    // P V MFMA i (0..11) of key half m: o0 for dims 0-31, o1 for 32-63,
+    // smallest products first.
+    auto pv_mfma = [&](int m, int i, const bf16x8 (&va)[3], const bf16x8 (&vc)[3], const bf16x8 (&pp)[3][2]) {
+        constexpr int vp[6] = {2, 1, 0, 1, 0, 0}, ppl[6] = {0, 1, 2, 0, 1, 0};
+        if (i % 2 == 0)
+            o0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(va[vp[i / 2]], pp[ppl[i / 2]][m], o0, 0, 0, 0);
+        else
+            o1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vc[vp[i / 2]], pp[ppl[i / 2]][m], o1, 0, 0, 0);
     };
 
     const int tiles = (n_k + AX_KT - 1) / AX_KT;
     const bool ragged = (n_k % AX_KT) != 0;
-    const int full = tiles - (ragged ? 1 : 0);
     const bool wave_active =
         qblock * (ATT_QW * ATT_WAVES) + __builtin_amdgcn_readfirstlane(wave) * ATT_QW < n_q;
-    fetch(0);
-    stage(0);
-    __syncthreads();
-    for (int t = 0; t < full; ++t) {
-        const int buf = t & 1;
-        const bool more = t + 1 < tiles;
-        fetch(min(t + 1, tiles - 1) * AX_KT);
+
+    // Tile t of the pipelined run (t + 1 < tiles). cur holds tile t's raw
+    // scores and mrow their row max; nxt and mrow receive tile t + 1's.
+    // Scheduling fences fix the instruction order: each of the 24 score
+    // MFMAs of tile t + 1 is followed by a share of tile t's softmax (one
+    // exponential and one row-sum add on each of the first 16, then the
+    // plane splits of one key pair each), and each k-group's K reads go out
+    // a k-group ahead; the row max of tile t + 1 runs between tile t's P V
+    // MFMAs. Then the staging of K tile t + 2 and V^T tile t + 1: K buffer
+    // t & 1 last held tile t and V^T buffer (t + 1) & 1 tile t - 1, both read
+    // before the last barrier.
+    auto pipelined = [&](int t, floatx16 &cur, floatx16 &nxt, float &mrow) {
+        if (t + 2 < tiles) fetch_k((t + 2) * AX_KT);
+        fetch_v((t + 1) * AX_KT);
         __builtin_amdgcn_sched_barrier(0);
-        if (wave_active) tile(std::false_type{}, buf, t * AX_KT);
-        if (more) {
-            // The other buffer was last read in tile t-1, which every wave
-            // finished before the previous barrier.
-            stage(buf ^ 1);
-            __syncthreads();
+        if (wave_active) {
+            raise_max(mrow);
+            const int kb = (t + 1) & 1, vb = t & 1;
+            float lsum = 0.0f;
+            uintx4 pw[3][2];
+            bf16x8 kf[2][3];
+            floatx16 acc = zero;
+            read_k(kb, 0, kf[0]);
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int s = 0; s < 24; ++s) {
+                const int t4 = s / 6, i = s % 6;
+                acc = score_mfma(t4, i, kf[t4 & 1], acc);
+                if (i == 0 && t4 < 3) read_k(kb, t4 + 1, kf[(t4 + 1) & 1]);
+                if (s < 16) cur[s] = __builtin_amdgcn_exp2f(cur[s] - mb);
+                if (s >= 1 && s <= 16) lsum += cur[s - 1];
+                if (s >= 16) split_pair(cur, s - 16, pw);
+                if (s == 23) l_run += att_pair_sum(lsum);
+                __builtin_amdgcn_sched_barrier(0);
+            }
+            nxt = acc;
+            bf16x8 pp[3][2];
+            planes_of(pw, pp);
+            float mx = 0.0f;
+#pragma unroll
+            for (int m = 0; m < 2; ++m) {
+                bf16x8 va[3], vc[3];
+                read_v(vb, m, va, vc);
+                __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+                for (int i = 0; i < 12; ++i) {
+                    pv_mfma(m, i, va, vc, pp);
+                    const int s = 12 * m + i;
+                    if (s == 2) mx = fmaxf(nxt[0], nxt[1]);
+                    if (s >= 3 && s <= 9) mx = fmaxf(fmaxf(mx, nxt[2 * s - 4]), nxt[2 * s - 3]);
+                    if (s == 10) mrow = att_pair_max(mx);
+                    __builtin_amdgcn_sched_barrier(0);
+                }
+            }
         }
+        __builtin_amdgcn_sched_barrier(0);
+        if (t + 2 < tiles) stage_k(t & 1);
+        stage_v((t + 1) & 1);
+        __syncthreads();
+    };
+    // The last tile (masked past n_k when ragged), not overlapped.
+    auto last = [&](int t, floatx16 &cur) {
+        if (!wave_active) return;
+        if (ragged) {
+#pragma unroll
+            for (int r = 0; r < 16; ++r)
+                if (t * AX_KT + 8 * (r >> 2) + 4 * half + (r & 3) >= n_k) cur[r] = -INFINITY;
+        }
+        raise_max(row_max(cur));
+        float lsum = 0.0f;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            cur[r] = __builtin_amdgcn_exp2f(cur[r] - mb);
+            lsum += cur[r];
+        }
+        l_run += att_pair_sum(lsum);
+        uintx4 pw[3][2];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) split_pair(cur, u, pw);
+        bf16x8 pp[3][2];
+        planes_of(pw, pp);
+#pragma unroll
+        for (int m = 0; m < 2; ++m) {
+            bf16x8 va[3], vc[3];
+            read_v(t & 1, m, va, vc);
+#pragma unroll
+            for (int i = 0; i < 12; ++i) pv_mfma(m, i, va, vc, pp);
+        }
+    };
+
+    // Prologue: K and V^T of tile 0 and K of tile 1 staged; tile 0's scores.
+    // The second barrier: K buffer 0 takes tile 2 at the end of the first
+    // tile, after every wave has read tile 0 from it.
+    fetch_k(0);
+    fetch_v(0);
+    stage_k(0);
+    stage_v(0);
+    if (tiles > 1) {
+        fetch_k(AX_KT);
+        stage_k(1);
     }
-    if (ragged && wave_active) tile(std::true_type{}, full & 1, full * AX_KT);
+    __syncthreads();
+    floatx16 sa = zero, sb = zero;
+    float mrow = 0.0f;
+    if (wave_active) {
+        sa = scores(0);
+        mrow = row_max(sa);
+    }
+    __syncthreads();
+    // Two tiles per trip, so the two score registers swap roles without
+    // copies.
+    int t = 0;
+    for (; t + 2 < tiles; t += 2) {
+        pipelined(t, sa, sb, mrow);
+        pipelined(t + 1, sb, sa, mrow);
+    }
+    if (t + 1 < tiles) {
+        pipelined(t, sa, sb, mrow);
+        last(t + 1, sb);
+    } else {
+        last(t, sa);
+    }
 
     if (!q_ok) return;
     const float inv = l_run > 0.0f ? 1.0f / l_run : 1.0f;

@@ -137,19 +137,42 @@ __device__ __forceinline__ unsigned short bf16_split_step(float &x) {
     x -= (float)h;
     return __builtin_bit_cast(unsigned short, h);
 }
+// Two values -> P planes as packed pairs, the same bits as bf16_split_step
+// on each: w[q] holds plane q of a0 (low half) and of a1 (high half). One
+// v_cvt_pk_bf16_f32 per plane; the residuals take the planes' bits straight
+// from the packed pair.
+template <int P>
+__device__ __forceinline__ void split_pair_planes(float a0, float a1, unsigned (&w)[P]) {
+    typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+    typedef float floatx2_t __attribute__((ext_vector_type(2)));
+#pragma unroll
+    for (int q = 0; q < P; ++q) {
+        const unsigned u = __builtin_bit_cast(unsigned, __builtin_convertvector((floatx2_t){a0, a1}, bf16x2_t));
+        w[q] = u;
+        if (q + 1 < P) {
+            a0 -= __builtin_bit_cast(float, u << 16);
+            a1 -= __builtin_bit_cast(float, u & 0xffff0000u);
+        }
+    }
+}
 // Four consecutive values -> P planes, 8 bytes per plane at dst + q * stride.
 template <int P>
 __device__ __forceinline__ void store_planes4(unsigned short *dst, int64_t stride, float4 v) {
-    float r[4] = {v.x, v.y, v.z, v.w};
+    unsigned lo[P], hi[P];
+    split_pair_planes<P>(v.x, v.y, lo);
+    split_pair_planes<P>(v.z, v.w, hi);
+#pragma unroll
+    for (int q = 0; q < P; ++q) *reinterpret_cast<uint2 *>(dst + q * stride) = make_uint2(lo[q], hi[q]);
+}
+// Two values -> P planes, a0's at dst + q * stride and a1's `step` further.
+template <int P>
+__device__ __forceinline__ void store_planes2(unsigned short *dst, int64_t step, int64_t stride, float a0, float a1) {
+    unsigned w[P];
+    split_pair_planes<P>(a0, a1, w);
 #pragma unroll
     for (int q = 0; q < P; ++q) {
-        unsigned short h[4];
-#pragma unroll
-        for (int e = 0; e < 4; ++e) h[e] = bf16_split_step(r[e]);
-        uint2 packed;
-        packed.x = (unsigned)h[0] | ((unsigned)h[1] << 16);
-        packed.y = (unsigned)h[2] | ((unsigned)h[3] << 16);
-        *reinterpret_cast<uint2 *>(dst + q * stride) = packed;
+        dst[q * stride] = (unsigned short)w[q];
+        dst[q * stride + step] = (unsigned short)(w[q] >> 16);
     }
 }
 // One value -> P planes.

@@ -604,21 +604,8 @@ struct EpLinear {
     double *stats;
     int64_t ldo, batch_stride;
     int tail;
-    unsigned short *planes_out = nullptr;
-    int64_t plane_stride = 0;
-    int planes = 0;
     MomentAcc acc;
     __device__ void init(int) {}
-    __device__ void put(int64_t at, float a) {
-        if (planes_out) {
-            if (planes == 3)
-                store_planes1<3>(planes_out + at, plane_stride, a);
-            else
-                store_planes1<1>(planes_out + at, plane_stride, a);
-        } else {
-            out[at] = a;
-        }
-    }
     __device__ void store(int z, int m, int n, float v) {
         int64_t at = z * batch_stride + (int64_t)m * ldo + n;
         float a = v + bias[n];
@@ -628,7 +615,7 @@ struct EpLinear {
             a = residual[at] + a * gamma[n];
             if (stats) acc.add(a);
         }
-        put(at, a);
+        out[at] = a;
     }
     // A wave's TM x TN fragments of a tile that lies wholly in range:
     // fragment (i, j) register r is row mb + 32 i + 8 (r / 4) + 4 khalf + r % 4,
@@ -662,24 +649,6 @@ struct EpLinear {
                     }
                 }
             }
-        } else if (planes_out) {
-            // Plane outputs, bias (+ GELU) tails.
-            unsigned short *po = planes_out + z * batch_stride;
-#pragma unroll
-            for (int j = 0; j < TN; ++j) {
-                const float bn = bias[nb + 32 * j + col];
-#pragma unroll
-                for (int i = 0; i < TM; ++i)
-#pragma unroll
-                    for (int r = 0; r < 16; ++r) {
-                        float a = v[i][j][r] + bn;
-                        if (tail == TAIL_BIAS_GELU) a = gelu(a);
-                        if (planes == 3)
-                            store_planes1<3>(po + at(i, j, r), plane_stride, a);
-                        else
-                            store_planes1<1>(po + at(i, j, r), plane_stride, a);
-                    }
-            }
         } else if (tail == TAIL_BIAS_GELU) {
 #pragma unroll
             for (int j = 0; j < TN; ++j) {
@@ -702,6 +671,53 @@ struct EpLinear {
     }
     __device__ void finalize(int z) {
         if (stats) acc.flush(stats + 2 * z);
+    }
+};
+
+// Epilogue of a linear whose output feeds the next plane GEMM (the
+// transformer FFN's first linear): GELU(acc + bias) as P bf16 planes, plane
+// q at out + q * plane_stride. A fixed tail and plane count keep the stores
+// branch-free, so the GELU chains of neighbouring elements interleave;
+// registers r and r + 1 (rows m and m + 1 of one column) share one
+// v_cvt_pk_bf16_f32 per plane.
+template <int P>
+struct EpGeluPlanes {
+    unsigned short *out;
+    const float *bias;
+    int64_t ldo, batch_stride, plane_stride;
+    __device__ void init(int) {}
+    __device__ void finalize(int) {}
+    __device__ void store(int z, int m, int n, float v) {
+        store_planes1<P>(out + z * batch_stride + (int64_t)m * ldo + n, plane_stride, gelu(v + bias[n]));
+    }
+    // Each plane's base is the wave tile's first row, and a lane's offsets
+    // within the tile are 32-bit, so no 64-bit address per store stays live.
+    template <int TM, int TN>
+    __device__ __forceinline__ void store_frags(int z, int mb, int nb, int col, int khalf,
+                                                const floatx16 (&v)[TM][TN]) {
+        unsigned short *base[P];
+#pragma unroll
+        for (int q = 0; q < P; ++q) base[q] = out + q * plane_stride + z * batch_stride + (int64_t)mb * ldo + nb;
+        const unsigned ld = (unsigned)ldo, lane = 4 * khalf * ld + col;
+#pragma unroll
+        for (int j = 0; j < TN; ++j) {
+            const float bn = bias[nb + 32 * j + col];
+#pragma unroll
+            for (int i = 0; i < TM; ++i)
+#pragma unroll
+                for (int r = 0; r < 16; r += 2) {
+                    const unsigned off = lane + (32 * i + 8 * (r / 4) + r % 4) * ld + 32 * j;
+                    unsigned w[P];
+                    split_pair_planes<P>(gelu(v[i][j][r] + bn), gelu(v[i][j][r + 1] + bn), w);
+#pragma unroll
+                    for (int q = 0; q < P; ++q) {
+                        base[q][off] = (unsigned short)w[q];
+                        base[q][off + ld] = (unsigned short)(w[q] >> 16);
+                    }
+                    // Four elements in flight at a time.
+                    if (r % 4 == 2) __builtin_amdgcn_sched_barrier(0);
+                }
+        }
     }
 };
 
@@ -1281,14 +1297,33 @@ void linear_planes(hipStream_t s, Planes x, int64_t ldx, int64_t x_batch_stride,
     require_ptrs({x.p, w.p, bias}, "linear_planes");
     DMX_REQUIRE(x.count == w.count && (x.count == 1 || x.count == 3), "linear_planes: 1 or 3 planes on both operands");
     if (out_planes.p) {
-        DMX_REQUIRE(tail != TAIL_RESIDUAL_SCALE && out_planes.count == x.count,
-                    "linear_planes: plane outputs take bias tails and the operands' plane count");
+        DMX_REQUIRE(tail == TAIL_BIAS_GELU && out_planes.count == x.count,
+                    "linear_planes: plane outputs take the bias + GELU tail and the operands' plane count");
         DMX_REQUIRE(out_planes.count == 1 || out_planes.stride >= (int64_t)batches * out_batch_stride,
                     "linear_planes: output planes overlap");
     } else {
         require_ptrs({out}, "linear_planes");
     }
     if (tail == TAIL_RESIDUAL_SCALE) require_ptrs({residual, gamma}, "linear residual");
+    // Batches laid end to end are one taller problem (whole tiles run over
+    // the batch boundaries), unless the epilogue keeps per-batch moments.
+    int64_t obs = out_batch_stride;
+    if (batches > 1 && !stats && x_batch_stride == (int64_t)M * ldx && out_batch_stride == (int64_t)M * ldo &&
+        (int64_t)M * batches < (1LL << 31)) {
+        M *= batches;
+        batches = 1;
+        obs = 0;
+    }
+    const PlaneRows al{x.p, ldx, x_batch_stride, x.stride}, bl{w.p, K, 0, w.stride};
+    if (out_planes.p) {
+        if (out_planes.count == 3)
+            launch_linear_planes(s, M, N, K, batches, al, bl, 3,
+                                 EpGeluPlanes<3>{out_planes.p, bias, ldo, obs, out_planes.stride});
+        else
+            launch_linear_planes(s, M, N, K, batches, al, bl, 1,
+                                 EpGeluPlanes<1>{out_planes.p, bias, ldo, obs, out_planes.stride});
+        return;
+    }
     EpLinear ep;
     ep.out = out;
     ep.bias = bias;
@@ -1296,21 +1331,9 @@ void linear_planes(hipStream_t s, Planes x, int64_t ldx, int64_t x_batch_stride,
     ep.gamma = gamma;
     ep.stats = stats;
     ep.ldo = ldo;
-    ep.batch_stride = out_batch_stride;
+    ep.batch_stride = obs;
     ep.tail = tail;
-    ep.planes_out = out_planes.p;
-    ep.plane_stride = out_planes.stride;
-    ep.planes = out_planes.count;
-    // Batches laid end to end are one taller problem (whole tiles run over
-    // the batch boundaries), unless the epilogue keeps per-batch moments.
-    if (batches > 1 && !stats && x_batch_stride == (int64_t)M * ldx && out_batch_stride == (int64_t)M * ldo &&
-        (int64_t)M * batches < (1LL << 31)) {
-        M *= batches;
-        batches = 1;
-        ep.batch_stride = 0;
-    }
-    launch_linear_planes(s, M, N, K, batches, PlaneRows{x.p, ldx, x_batch_stride, x.stride},
-                         PlaneRows{w.p, K, 0, w.stride}, x.count, ep);
+    launch_linear_planes(s, M, N, K, batches, al, bl, x.count, ep);
 }
 
 void linear_qkv_planes(hipStream_t s, Planes x, int64_t ldx, int64_t x_batch_stride, Planes w, const float *bias,
