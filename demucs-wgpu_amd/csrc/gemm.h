@@ -91,16 +91,13 @@ struct GemmStage<3> {
 };
 
 // Four values -> three bf16 planes (round to nearest even at each step), as
-// bits, four per uint2.
+// bits, four per uint2: two pairs, one v_cvt_pk_bf16_f32 per pair and plane.
 __device__ __forceinline__ void split_planes4(float4 v, uint2 (&out)[3]) {
-    float r[4] = {v.x, v.y, v.z, v.w};
+    unsigned lo[3], hi[3];
+    split_pair_planes<3>(v.x, v.y, lo);
+    split_pair_planes<3>(v.z, v.w, hi);
 #pragma unroll
-    for (int q = 0; q < 3; ++q) {
-        unsigned short h[4];
-#pragma unroll
-        for (int e = 0; e < 4; ++e) h[e] = bf16_split_step(r[e]);
-        out[q] = make_uint2((unsigned)h[0] | ((unsigned)h[1] << 16), (unsigned)h[2] | ((unsigned)h[3] << 16));
-    }
+    for (int q = 0; q < 3; ++q) out[q] = make_uint2(lo[q], hi[q]);
 }
 
 // An m/n-major loader may fetch four consecutive k of one column at once
