@@ -243,7 +243,10 @@ def test_dconv_both_layers_matches_oracle(lib, oracle, dmx, B, C, F, T):
     assert rms_relative_error(ref, dx.cpu().numpy()) < 1e-5
 
 
-@pytest.mark.parametrize("batch,heads,nq,nk", [(1, 8, 200, 130), (2, 2, 64, 64), (1, 1, 33, 1), (1, 8, 2688, 1344)])
+# Key counts cover one to five 32-key tiles, whole and ragged, so the
+# three-plane kernel's pipelined loop runs with odd and even tile counts.
+@pytest.mark.parametrize("batch,heads,nq,nk", [(1, 8, 200, 130), (2, 2, 64, 64), (1, 1, 33, 1), (1, 8, 2688, 1344),
+                                               (1, 2, 50, 32), (1, 2, 40, 40), (1, 2, 70, 96), (2, 1, 65, 128)])
 def test_attention_matches_oracle(lib, oracle, fp32_precision, batch, heads, nq, nk):
     r = rng(nq + nk)
     D = heads * 64
