@@ -825,9 +825,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void a
     // Scheduling fences fix the instruction order: each of the 24 score
     // MFMAs of tile t + 1 is followed by a share of tile t's softmax (one
     // exponential and one row-sum add on each of the first 16, then the
-    // plane splits of one key pair each), and each k-group's K reads go out
-    // a k-group ahead; the row max of tile t + 1 runs between tile t's P V
-    // MFMAs. Then the staging of K tile t + 2 and V^T tile t + 1: K buffer
+    // plane splits of one key pair each), each k-group's K reads go out a
+    // k-group ahead, and the first key half's V^T fragments during the last
+    // score MFMAs (the second half's after the first P V MFMA); the row max
+    // of tile t + 1 runs between tile t's P V MFMAs. Then the staging of K tile t + 2 and V^T tile t + 1: K buffer
     // t & 1 last held tile t and V^T buffer (t + 1) & 1 tile t - 1, both read
     // before the last barrier.
     auto pipelined = [&](int t, floatx16 &cur, floatx16 &nxt, float &mrow) {
@@ -840,6 +841,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void a
             float lsum = 0.0f;
             uintx4 pw[3][2];
             bf16x8 kf[2][3];
+            bf16x8 va[2][3], vc[2][3];
             floatx16 acc = zero;
             read_k(kb, 0, kf[0]);
             __builtin_amdgcn_sched_barrier(0);
@@ -848,6 +850,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void a
                 const int t4 = s / 6, i = s % 6;
                 acc = score_mfma(t4, i, kf[t4 & 1], acc);
                 if (i == 0 && t4 < 3) read_k(kb, t4 + 1, kf[(t4 + 1) & 1]);
+                // V^T fragments of the first key half, ahead of the P V MFMAs.
+                if (s == 19) read_v(vb, 0, va[0], vc[0]);
                 if (s < 16) cur[s] = __builtin_amdgcn_exp2f(cur[s] - mb);
                 if (s >= 1 && s <= 16) lsum += cur[s - 1];
                 if (s >= 16) split_pair(cur, s - 16, pw);
@@ -860,12 +864,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void a
             float mx = 0.0f;
 #pragma unroll
             for (int m = 0; m < 2; ++m) {
-                bf16x8 va[3], vc[3];
-                read_v(vb, m, va, vc);
-                __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
                 for (int i = 0; i < 12; ++i) {
-                    pv_mfma(m, i, va, vc, pp);
+                    pv_mfma(m, i, va[m], vc[m], pp);
+                    // The second key half's fragments after the first MFMA.
+                    if (m == 0 && i == 0) read_v(vb, 1, va[1], vc[1]);
                     const int s = 12 * m + i;
                     if (s == 2) mx = fmaxf(nxt[0], nxt[1]);
                     if (s >= 3 && s <= 9) mx = fmaxf(fmaxf(mx, nxt[2 * s - 4]), nxt[2 * s - 3]);
