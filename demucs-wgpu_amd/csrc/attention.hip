@@ -828,9 +828,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void a
     // plane splits of one key pair each), each k-group's K reads go out a
     // k-group ahead, and the first key half's V^T fragments during the last
     // score MFMAs (the second half's after the first P V MFMA); the row max
-    // of tile t + 1 runs between tile t's P V MFMAs. Then the staging of K tile t + 2 and V^T tile t + 1: K buffer
-    // t & 1 last held tile t and V^T buffer (t + 1) & 1 tile t - 1, both read
-    // before the last barrier.
+    // of tile t + 1 runs between tile t's P V MFMAs. Then the staging of K
+    // tile t + 2 and V^T tile t + 1: K buffer t & 1 last held tile t and V^T
+    // buffer (t + 1) & 1 tile t - 1, both read before the last barrier.
     auto pipelined = [&](int t, floatx16 &cur, floatx16 &nxt, float &mrow) {
         if (t + 2 < tiles) fetch_k((t + 2) * AX_KT);
         fetch_v((t + 1) * AX_KT);
