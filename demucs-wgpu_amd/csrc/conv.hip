@@ -691,7 +691,8 @@ struct EpGeluPlanes {
         store_planes1<P>(out + z * batch_stride + (int64_t)m * ldo + n, plane_stride, gelu(v + bias[n]));
     }
     // Each plane's base is the wave tile's first row, and a lane's offsets
-    // within the tile are 32-bit, so no 64-bit address per store stays live.
+    // within the tile are 32-bit (the host keeps 256 rows of ldo below 2^31),
+    // so no 64-bit address per store stays live.
     template <int TM, int TN>
     __device__ __forceinline__ void store_frags(int z, int mb, int nb, int col, int khalf,
                                                 const floatx16 (&v)[TM][TN]) {
@@ -1301,6 +1302,7 @@ void linear_planes(hipStream_t s, Planes x, int64_t ldx, int64_t x_batch_stride,
                     "linear_planes: plane outputs take the bias + GELU tail and the operands' plane count");
         DMX_REQUIRE(out_planes.count == 1 || out_planes.stride >= (int64_t)batches * out_batch_stride,
                     "linear_planes: output planes overlap");
+        DMX_REQUIRE(ldo > 0 && ldo * 256 < (1LL << 31), "linear_planes: plane output rows too long");
     } else {
         require_ptrs({out}, "linear_planes");
     }
