@@ -145,7 +145,7 @@ void split_to_planes(hipStream_t s, const float *x, int64_t n, Planes out);
 // linear() over plane operands on the bf16 matrix cores (gemm_planes.h):
 // x rows at z * x_batch_stride + m * ldx of every plane, W (N, K) row-major
 // planes. The result goes to `out` (fp32), or, when out_planes.p is set, to
-// out_planes (same indexing) and `out` is unused. Plane products (i, j) with
+// out_planes (same indexing; the bias + GELU tail only) and `out` is unused. Plane products (i, j) with
 // i + j < count are summed, so count = 3 is an fp32-accurate product.
 void linear_planes(hipStream_t s, Planes x, int64_t ldx, int64_t x_batch_stride, Planes w, const float *bias,
                    int batches, int M, int K, int N, float *out, Planes out_planes, int64_t ldo,
